@@ -1,0 +1,249 @@
+#!/usr/bin/env python3
+"""Throughput of the AWQ INT4 hot path on one MI355X.
+
+Headline (`value`): decode dequant-GEMV at M=1 on the Llama-3-8B gate/up shape
+(K=4096 -> N=14336, group 128; f32 activations ~N(0,1), f16 scales
+U[0.002, 0.02], uniform 4-bit weights/zeros in AutoAWQ packing, f32 output),
+in GB/s of algorithmic HBM bytes per call:
+    K*N/2 + (K/g)*(N/8)*4 + (K/g)*N*2 + M*K*4 + M*N*4  = 30,580,736 B.
+Secondary objects in the same JSON line: prefill at M=2048 on the same shape
+(fp16 activations, fp16 MFMA, fp32 accumulation; TFLOP/s of 2*M*N*K) and the
+standalone dequantize of K=14336, N=4096, g64 (f32 out; GB/s of read+write).
+
+Method: inputs resident in HBM before timing; the decode rotates over
+ceil(512 MB / bytes-per-call) independent weight copies so the 256 MB MALL
+cannot serve them. Calls are captured in a HIP graph (one graph = many
+back-to-back launches on the stream) and the graph is replayed; HIP events on
+that stream bracket the timed replays, after `--warmup` untimed calls and a
+device synchronise on both sides. `roofline.achieved` = algorithmic bytes
+(flops) per launch / average launch duration from those events.
+cpu_baseline: the oracle's C restatement of the reference's f32 loop on the
+host cores (OpenMP), on a bounded sample of the same decode workload.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "cube-awq_amd"))
+
+METRIC = "M=1 decode GB/s (% of HBM peak) + M=2048 prefill TFLOPS, 4096x14336 AWQ g128"
+HBM_PEAK_GBS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X published figure
+TRAFFIC_FILE = os.path.join(REPO, "profiles", "hbm_traffic.json")
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20000, help="timed decode calls")
+    ap.add_argument("--warmup", type=int, default=500, help="untimed decode calls")
+    ap.add_argument("--only", choices=["decode", "prefill", "dequant"], default=None,
+                    help="run one workload only (profiling runs)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(the per-GPU shard is the single-GPU kernel; see DESIGN.md).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import cube_awq
+    from cube_awq import _lib, synth
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    L = cube_awq.lib()
+
+    def cur_stream():
+        # the stream torch is issuing on (the capture stream inside torch.cuda.graph)
+        return torch.cuda.current_stream().cuda_stream
+
+    def call_gemm(x, xt, qw, qz, sc, st, y, yt, M, K, N, g):
+        rc = L.awq_gemm(x.data_ptr(), xt, qw.data_ptr(), qz.data_ptr(), sc.data_ptr(), st, None,
+                        _lib.AWQ_F32, y.data_ptr(), yt, M, K, N, g, cur_stream())
+        if rc:
+            _lib.check(rc)
+
+    run_stream = torch.cuda.Stream()  # warm-up, capture, replay and events all on it
+
+    def graph_time(launch, per_graph, warmup, steps):
+        """ms per call: `launch(i)` captured `per_graph` times into a graph,
+        replayed until `steps` calls; events on the launch stream."""
+        torch.cuda.synchronize()
+        with torch.cuda.stream(run_stream):
+            # Warm-up on the capture stream: the library's per-stream split-K
+            # workspace is allocated here, never inside the capture.
+            for i in range(max(warmup, 1)):
+                launch(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=run_stream):
+            for i in range(per_graph):
+                launch(i)
+        reps = max(1, math.ceil(steps / per_graph))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(run_stream):
+            g.replay()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            e0.record(run_stream)
+            for _ in range(reps):
+                g.replay()
+            e1.record(run_stream)
+            e1.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ms = e0.elapsed_time(e1) / (reps * per_graph)
+        return ms, reps * per_graph, wall
+
+    out = {}
+    traffic = {}
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f)
+
+    # ---------------- decode M=1, 4096 -> 14336 -------------------------------------------
+    M, K, N, G = 1, 4096, 14336, 128
+    dec_bytes = K * N // 2 + (K // G) * (N // 8) * 4 + (K // G) * N * 2 + M * K * 4 + M * N * 4
+    if args.only in (None, "decode"):
+        qw = torch.from_numpy(synth.packed_nibbles(synth.TID_QWEIGHT, K, N // 8).view(np.int32)).to(dev)
+        qz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, K // G, N // 8).view(np.int32)).to(dev)
+        sc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (K // G, N), 0.002, 0.02, np.float16)).to(dev)
+        x = torch.from_numpy(synth.normal(synth.TID_X, (M, K), np.float32)).to(dev)
+        copies = math.ceil(512e6 / dec_bytes)
+        ws = [(qw.clone(), qz.clone(), sc.clone()) for _ in range(copies)]
+        y = torch.empty((M, N), dtype=torch.float32, device=dev)
+
+        def dec(i):
+            w = ws[i % copies]
+            call_gemm(x, _lib.AWQ_F32, w[0], w[1], w[2], _lib.AWQ_F16, y, _lib.AWQ_F32, M, K, N, G)
+
+        ms, calls, wall = graph_time(dec, copies * 6, args.warmup, args.steps)
+        gbs = dec_bytes / (ms * 1e-3) / 1e9
+        out["decode"] = dict(ms=ms, calls=calls, wall_s=wall, gbs=gbs, bytes=dec_bytes, copies=copies)
+        del ws
+
+    # ---------------- prefill M=2048, 4096 -> 14336 ---------------------------------------
+    PM = 2048
+    pf_flops = 2.0 * PM * N * K
+    if args.only in (None, "prefill"):
+        qw = torch.from_numpy(synth.packed_nibbles(synth.TID_QWEIGHT, K, N // 8).view(np.int32)).to(dev)
+        qz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, K // G, N // 8).view(np.int32)).to(dev)
+        sc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (K // G, N), 0.002, 0.02, np.float16)).to(dev)
+        xp = torch.from_numpy(synth.normal(synth.TID_X, (PM, K), np.float16)).to(dev)
+        yp = torch.empty((PM, N), dtype=torch.float16, device=dev)
+
+        def pre(i):
+            call_gemm(xp, _lib.AWQ_F16, qw, qz, sc, _lib.AWQ_F16, yp, _lib.AWQ_F16, PM, K, N, G)
+
+        steps = 50 if args.only is None else max(10, args.steps // 100)
+        ms, calls, wall = graph_time(pre, 10, 5, steps)
+        out["prefill"] = dict(ms=ms, calls=calls, wall_s=wall, tflops=pf_flops / (ms * 1e-3) / 1e12)
+
+    # ---------------- dequantize K=14336, N=4096, g64 -------------------------------------
+    DK, DN, DG = 14336, 4096, 64
+    dq_bytes = DK * DN // 2 + (DK // DG) * DN // 2 + (DK // DG) * DN * 4 + DK * DN * 4
+    if args.only in (None, "dequant"):
+        dqw = torch.from_numpy(synth.packed_nibbles(synth.TID_QWEIGHT, DK, DN // 8).view(np.int32)).to(dev)
+        dqz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, DK // DG, DN // 8).view(np.int32)).to(dev)
+        dsc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (DK // DG, DN), 0.002, 0.02, np.float32)).to(dev)
+        dout = torch.empty((DK, DN), dtype=torch.float32, device=dev)
+
+        def deq(i):
+            rc = L.awq_dequantize(dqw.data_ptr(), dqz.data_ptr(), dsc.data_ptr(), _lib.AWQ_F32,
+                                  dout.data_ptr(), _lib.AWQ_F32, DK, DN, DG,
+                                  _lib.AWQ_ORDER_SEQUENTIAL, cur_stream())
+            if rc:
+                _lib.check(rc)
+
+        steps = 200 if args.only is None else max(20, args.steps // 20)
+        ms, calls, wall = graph_time(deq, 20, 10, steps)
+        out["dequant"] = dict(ms=ms, calls=calls, wall_s=wall, gbs=dq_bytes / (ms * 1e-3) / 1e9,
+                              bytes=dq_bytes)
+
+    # ---------------- CPU baseline (oracle, host cores) -----------------------------------
+    cpu = None
+    if not args.no_cpu_baseline and args.only in (None, "decode"):
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        import awq_oracle as oracle
+        hx = synth.normal(synth.TID_X, (M, K), np.float32)
+        hqw = synth.packed_nibbles(synth.TID_QWEIGHT, K, N // 8)
+        hqz = synth.packed_nibbles(synth.TID_QZEROS, K // G, N // 8)
+        hsc = synth.uniform(synth.TID_SCALES, (K // G, N), 0.002, 0.02, np.float16).astype(np.float32)
+        oracle.gemm_f32(hx, hqw, hqz, hsc, G)  # warm-up
+        n = 0
+        t0 = time.perf_counter()
+        while True:
+            oracle.gemm_f32(hx, hqw, hqz, hsc, G)
+            n += 1
+            el = time.perf_counter() - t0
+            if el >= args.cpu_seconds and n >= 3:
+                break
+        cpu = dict(value=dec_bytes / (el / n) / 1e9, unit="GB/s", cores=oracle.num_threads(),
+                   kind="port",
+                   sample=f"{n} calls of the M=1 4096x14336 g128 decode (oracle f32 loop, "
+                          f"{el:.1f} s, OpenMP over {oracle.num_threads()} threads)")
+
+    res = {
+        "metric": METRIC,
+        "value": None,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: SplitMix64-seeded uniform 4-bit weights/zeros (AutoAWQ packing), "
+                "N(0,1) activations, U[0.002,0.02] scales",
+        "config": {"workload": "AWQ decode dequant-GEMV M=1, K=4096 -> N=14336 (Llama-3-8B "
+                               "gate/up), group 128, f32 activations, f16 scales, f32 output",
+                   "M": M, "K": K, "N": N, "group_size": G, "parallelism": "single GPU"},
+    }
+    if "decode" in out:
+        d = out["decode"]
+        res["value"] = round(d["gbs"], 2)
+        res["ms_per_step"] = d["ms"]
+        res["steps"] = d["calls"]
+        tr = traffic.get("decode_m1_4096x14336")
+        res["roofline"] = {"bound": "hbm", "achieved": round(d["gbs"], 2), "peak": HBM_PEAK_GBS,
+                           "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                           "traffic": tr, "algorithmic_bytes": dec_bytes,
+                           "rotating_copies": d["copies"], "us_per_call": round(d["ms"] * 1e3, 3)}
+    if cpu:
+        res["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()}
+    if "prefill" in out:
+        p = out["prefill"]
+        res["prefill_m2048"] = {"tflops": round(p["tflops"], 2), "ms_per_call": round(p["ms"], 4),
+                                "roofline": {"bound": "mfma", "achieved": round(p["tflops"], 2),
+                                             "peak": FP16_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                             "frac": round(p["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4),
+                                             "traffic": traffic.get("prefill_m2048_4096x14336")},
+                                "dtype": "f16 in, fp32 accumulate, f16 out", "calls": p["calls"]}
+    if "dequant" in out:
+        q = out["dequant"]
+        res["dequant_k14336_n4096_g64"] = {
+            "gbs": round(q["gbs"], 2), "us_per_call": round(q["ms"] * 1e3, 2),
+            "roofline": {"bound": "hbm", "achieved": round(q["gbs"], 2), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(q["gbs"] / HBM_PEAK_GBS, 4),
+                         "traffic": traffic.get("dequant_14336x4096_g64")},
+            "calls": q["calls"]}
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,169 @@
+// awq_common.h -- shared host/device definitions of the gfx950 AWQ library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/awq.h"
+
+namespace cube_awq {
+
+// ---------------------------------------------------------------------------
+// Host-side error plumbing. A failed assertion throws Panic carrying the exact
+// text the reference panics with; the C ABI turns it into AWQ_ERR_INVALID and
+// awq_last_error().
+// ---------------------------------------------------------------------------
+struct Panic {
+  std::string msg;
+};
+struct HipFailure {
+  std::string msg;
+};
+
+[[noreturn]] void panic(const std::string& msg);
+void check_hip(hipError_t e, const char* what);
+
+// Rust `assert!(cond, "msg")` -> panics with "msg".
+#define AWQ_ASSERT(cond, msg)                  \
+  do {                                         \
+    if (!(cond)) ::cube_awq::panic((msg));     \
+  } while (0)
+
+// Rust `assert_eq!(a, b, "msg")` -> "assertion `left == right` failed: msg\n  left: a\n right: b".
+std::string assert_eq_text(const std::string& msg, long long left, long long right);
+#define AWQ_ASSERT_EQ(a, b, msg)                                                         \
+  do {                                                                                  \
+    long long _l = (long long)(a), _r = (long long)(b);                                 \
+    if (_l != _r) ::cube_awq::panic(::cube_awq::assert_eq_text((msg), _l, _r));         \
+  } while (0)
+
+constexpr int dtype_size_ct(int32_t t) {
+  switch (t) {
+    case AWQ_F32: return 4;
+    case AWQ_F16: return 2;
+    case AWQ_BF16: return 2;
+    case AWQ_U32: return 4;
+    case AWQ_I32: return 4;
+    case AWQ_I16: return 2;
+    case AWQ_I64: return 8;
+    default: return 0;
+  }
+}
+inline int dtype_size(int32_t t) { return dtype_size_ct(t); }
+inline bool is_float_dtype(int32_t t) { return t == AWQ_F32 || t == AWQ_F16 || t == AWQ_BF16; }
+
+// ---------------------------------------------------------------------------
+// Device element helpers.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16_t;
+typedef __bf16 bf16_t;
+
+template <int T> struct Elem;
+template <> struct Elem<AWQ_F32> { typedef float type; };
+template <> struct Elem<AWQ_F16> { typedef f16_t type; };
+template <> struct Elem<AWQ_BF16> { typedef bf16_t type; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(f16_t v) { return (float)v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+  // bf16 -> f32 is exact: the bf16 bits are the high half of the f32.
+  return __builtin_bit_cast(float, ((uint32_t)__builtin_bit_cast(uint16_t, v)) << 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
+  return (f16_t)v;  // v_cvt_f16_f32, round to nearest even
+}
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+  return (bf16_t)v;  // v_cvt_pk_bf16_f32 on gfx950, round to nearest even
+}
+
+// Runtime-typed scalar load/store for data touched outside the hot loops.
+__device__ __forceinline__ float load_f32_any(const void* p, int64_t i, int32_t t) {
+  if (t == AWQ_F32) return ((const float*)p)[i];
+  if (t == AWQ_F16) return to_f32(((const f16_t*)p)[i]);
+  return to_f32(((const bf16_t*)p)[i]);
+}
+__device__ __forceinline__ void store_f32_any(void* p, int64_t i, int32_t t, float v) {
+  if (t == AWQ_F32) ((float*)p)[i] = v;
+  else if (t == AWQ_F16) ((f16_t*)p)[i] = from_f32<f16_t>(v);
+  else ((bf16_t*)p)[i] = from_f32<bf16_t>(v);
+}
+
+// Raw buffer access: a 128-bit resource (base, byte size) in SGPRs plus a
+// per-lane byte offset (VGPR) and a wave-uniform byte offset (SGPR), so a
+// strided walk over rows costs no per-load VALU address arithmetic.
+// 0x00020000 is the gfx9-family dword3 (32-bit raw data format).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ uint32_t buf_load_u32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+// Same with the nontemporal (nt) cache policy: for data read exactly once
+// (the weight stream), so it does not displace reused lines in L2.
+constexpr int kCachePolicyNT = 2;
+__device__ __forceinline__ uint32_t buf_load_u32_nt(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kCachePolicyNT);
+}
+
+// AutoAWQ interleave: logical column c of a pack sits in packed lane
+// kAwqLaneOfCol[c]; packed lane p holds column kAwqColOfLane[p].
+// (Same table as the reference, src/kernel/awq_kernel_gemm.rs:7-30.)
+__host__ __device__ constexpr int awq_lane_of_col(int c) {
+  return (c == 0) ? 0 : (c == 1) ? 4 : (c == 2) ? 1 : (c == 3) ? 5
+       : (c == 4) ? 2 : (c == 5) ? 6 : (c == 6) ? 3 : 7;
+}
+__host__ __device__ constexpr int awq_col_of_lane(int p) {
+  return (p == 0) ? 0 : (p == 1) ? 2 : (p == 2) ? 4 : (p == 3) ? 6
+       : (p == 4) ? 1 : (p == 5) ? 3 : (p == 6) ? 5 : 7;
+}
+
+// ---------------------------------------------------------------------------
+// Launch descriptors shared by the API layer and the kernels.
+// ---------------------------------------------------------------------------
+struct GemmProblem {
+  const void* x;
+  int32_t xt;
+  const uint32_t* qweight;
+  const uint32_t* qzeros;
+  const void* scales;
+  int32_t st;
+  const void* bias;  // nullable, [N]
+  int32_t bt;
+  void* y;
+  int32_t yt;
+  int64_t rows;  // rows to compute and write (m_valid)
+  int64_t K, N, group;
+  hipStream_t stream;
+};
+
+struct DequantProblem {
+  const uint32_t* qweight;
+  const uint32_t* qzeros;
+  const void* scales;
+  int32_t st;
+  void* out;
+  int32_t ot;
+  int64_t K, N, group;
+  int32_t order;
+  hipStream_t stream;
+};
+
+// Kernel launchers (defined in the .hip translation units).
+void launch_dequant(const DequantProblem& p);
+void launch_gemv(const GemmProblem& p);   // rows <= 8
+void launch_gemm(const GemmProblem& p);   // rows > 8
+
+// Per-(device, stream, slot) device workspace, grown on demand and never shrunk.
+// kWsCounters is zero-filled when (re)allocated and kernels leave it zero;
+// kWsPartials holds split-K partial sums (contents undefined between calls).
+enum { kWsCounters = 0, kWsPartials = 1 };
+void* workspace_get(hipStream_t stream, size_t bytes, int slot);
+
+}  // namespace cube_awq

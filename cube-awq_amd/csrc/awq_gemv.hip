@@ -1,0 +1,445 @@
+// awq_gemv.hip -- decode path (M <= 8) of the fused AWQ dequant-GEMM for gfx950.
+//
+// y[m, n] = sum_k x[m, k] * (q[k, n] - z[k/g, n]) * s[k/g, n]   (AutoAWQ nibble order)
+// The reference's gemm_awq_decode (src/kernel/awq_kernel_gemm.rs:445-624) runs
+// one thread per (row, 16 columns) over the whole K in 64 threads per
+// workgroup, 112 workgroups for N = 14336. Here the kernel is shaped for HBM
+// bandwidth on 256 CUs:
+//
+//  * qweight is read row-contiguously: lane l of a wave owns packed word
+//    chunk*64 + l (8 columns), so a wave load reads 256 contiguous bytes of a
+//    row; a wave walks RPW consecutive rows of one quantisation group, which
+//    makes x[m, k] wave-uniform (scalar loads, SGPR operand of the FMAs).
+//    Every load a wave needs (its RPW weight words, one x value per lane for
+//    the activation sum, the zero word and the 8 scales) is issued up front,
+//    so a workgroup's whole share of qweight is in flight at once.
+//  * Per wave segment a[m, n] = sum_k x[m, k] * q[k, n] is accumulated and
+//    the zero point and scale folded once:
+//        acc[m, n] += s[g, n] * (a[m, n] - z[g, n] * sum_k x[m, k])
+//    the reference's sum of x * (q - z) * s with one FMA per weight.
+//  * Nibbles reach the FMA without a conversion instruction: AutoAWQ packs
+//    columns (0,1), (2,3), (4,5), (6,7) in packed lanes (0,4), (1,5), (2,6),
+//    (3,7), i.e. in the low nibble of the two 16-bit halves at bit offsets 0,
+//    4, 8, 12. Masking a word with 0x000F000F (or 0x00F000F0, and the same on
+//    the word shifted right by 8) leaves each half holding q (or 16q), which
+//    read as f16 is the exact denormal q * 2^-24; v_fma_mix_f32 widens it and
+//    accumulates x * q * 2^-24 in f32 with the same single rounding as
+//    x * q. Per 8 weights: 1 shift + 4 ands + 8 v_fma_mix_f32. The 2^-24
+//    (2^-20 for the 16q halves) is undone at the end (exact).
+//  * The waves of a workgroup (stacked along K) are summed through LDS in a
+//    fixed order. When K needs more than one workgroup per column chunk
+//    (grid.y = splits), each writes its partial and the last to arrive sums
+//    them in split order (handshake below); arrival counters sit on separate
+//    256-byte lines so chunks do not serialise on one line.
+//
+// Algorithmic HBM bytes per call: K*N/2 (qweight) + (K/g)*(N/8)*4 (qzeros) +
+// (K/g)*N*sizeof(scale) + M*K*sizeof(x) + M*N*sizeof(y).
+#include <cstdlib>
+
+#include "awq_common.h"
+
+namespace cube_awq {
+namespace {
+
+struct GemvArgs {
+  const void* x;
+  const uint32_t* qweight;
+  const uint32_t* qzeros;
+  const void* scales;
+  const void* bias;
+  void* y;
+  float* partial;     // [splits][MT][N] when splits > 1
+  uint32_t* counters; // one per chunk, kCounterStride apart, zero between calls
+  int32_t st, bt, yt;
+  int32_t rows;       // valid rows (<= MT)
+  int32_t K, N, group;
+  int32_t splits;
+};
+
+template <int XT>
+__device__ __forceinline__ float load_x(const void* x, int64_t i) {
+  using X = typename Elem<XT>::type;
+  return to_f32(static_cast<const X*>(x)[i]);
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Raw bytes of the 8 scales of one packed word: 32 bytes for f32 scales, 16
+// for f16/bf16 (the second load then repeats the first). Issued without any
+// dtype branch so no wait is placed before the weight stream.
+struct RawScales {
+  u32x4_t lo, hi;
+};
+__device__ __forceinline__ RawScales load_scales_raw(const void* scales, int32_t st, int64_t off) {
+  const int es = st == AWQ_F32 ? 4 : 2;
+  const char* p = static_cast<const char*>(scales) + off * es;
+  RawScales r;
+  r.lo = *reinterpret_cast<const u32x4_t*>(p);
+  r.hi = *reinterpret_cast<const u32x4_t*>(p + (es == 4 ? 16 : 0));
+  return r;
+}
+// Convert once the weights are consumed: column order, as floats. All three
+// interpretations are formed and one selected, so no branch (and no early
+// wait on the loads) is introduced.
+__device__ __forceinline__ void scales_to_f32(const RawScales& r, int32_t st, float (&sc)[8]) {
+  const bool is32 = st == AWQ_F32, is16 = st == AWQ_F16;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t word = r.lo[j >> 1];
+    const uint32_t half = (j & 1) ? (word >> 16) : (word & 0xFFFFu);
+    const float v32 = __builtin_bit_cast(float, (j < 4) ? r.lo[j] : r.hi[j - 4]);
+    const float v16 = (float)__builtin_bit_cast(f16_t, (uint16_t)half);
+    const float vb16 = __builtin_bit_cast(float, half << 16);
+    sc[j] = is32 ? v32 : (is16 ? v16 : vb16);
+  }
+}
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+// The 4 masked views of a packed word: element j holds columns (2j, 2j+1) as
+// f16 denormals q * 2^-24 (j = 0, 2) or 16q * 2^-24 (j = 1, 3).
+__device__ __forceinline__ void split_word(uint32_t w, uint32_t (&mk)[4]) {
+  const uint32_t w8 = w >> 8;
+  mk[0] = w & 0x000F000Fu;
+  mk[1] = w & 0x00F000F0u;
+  mk[2] = w8 & 0x000F000Fu;
+  mk[3] = w8 & 0x00F000F0u;
+}
+
+// acc[c] += x * (scaled q of column c) for the 8 columns of one word.
+__device__ __forceinline__ void fma_word(float (&acc)[8], float x, const uint32_t (&mk)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const h2_t h = __builtin_bit_cast(h2_t, mk[j]);
+    acc[2 * j] = fmaf(x, (float)h[0], acc[2 * j]);          // v_fma_mix_f32, low half
+    acc[2 * j + 1] = fmaf(x, (float)h[1], acc[2 * j + 1]);  // v_fma_mix_f32, high half
+  }
+}
+
+// The same scaled values as plain floats (used for the zero points).
+__device__ __forceinline__ void word_values(uint32_t w, float (&v)[8]) {
+  uint32_t mk[4];
+  split_word(w, mk);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const h2_t h = __builtin_bit_cast(h2_t, mk[j]);
+    v[2 * j] = (float)h[0];
+    v[2 * j + 1] = (float)h[1];
+  }
+}
+
+// Undo the denormal scaling of column c: 2^24 for q halves, 2^20 for 16q halves.
+__device__ __forceinline__ float col_unscale(int c) { return ((c >> 1) & 1) ? 1048576.0f : 16777216.0f; }
+
+
+
+constexpr int kCounterStride = 64;  // u32 words between arrival counters (256 B)
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int XT, int MT, int WAVES, int RPW>
+__global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
+  constexpr int kChunkCols = 512;  // 64 lanes x 8 columns
+  __shared__ float red[WAVES][MT][kChunkCols];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  // Wave-uniform by construction; readfirstlane lets the compiler know, so the
+  // K range, x addresses and group index live in SGPRs (x via scalar loads).
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int chunk = blockIdx.x;
+  const int split = blockIdx.y;
+  const int np = a.N >> 3;
+  const int pack = chunk * 64 + lane;
+  const bool lane_ok = pack < np;
+  const int pack_c = lane_ok ? pack : np - 1;  // clamped: loads stay in bounds
+  const int rows = a.rows;
+
+  // This wave's rows [k0, k0 + RPW): one run inside one quantisation group
+  // (RPW divides the group size, K is a multiple of the group size), so a
+  // wave's run is either entirely inside K or entirely past it.
+  const int k0 = (split * WAVES + wave) * RPW;
+  const bool live = k0 < a.K;
+  const int kc = live ? k0 : 0;  // row base for loads (row 0 for waves past K)
+  const int grp = kc / a.group;
+
+  int64_t xrow[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) xrow[m] = (int64_t)min(m, rows - 1) * a.K + kc;
+
+  // ---- loads, in the order they are consumed (vmcnt retires in issue order) ----
+  // 1. zero word and scales of the group, 2. one x per lane for the activation
+  // sum, 3. the RPW weight words (batches of RB, the next batch requested
+  // before the current one is consumed).
+  const uint32_t zw = a.qzeros[(int64_t)grp * np + pack_c];
+  const RawScales sraw = load_scales_raw(a.scales, a.st, (int64_t)grp * a.N + (int64_t)pack_c * 8);
+  float xl[MT];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    float v = 0.f;
+#pragma unroll
+    for (int h = 0; h < (RPW + 63) / 64; ++h) {
+      const int r = min(h * 64 + lane, RPW - 1);
+      const float t = load_x<XT>(a.x, xrow[m] + r);
+      v += (h * 64 + lane < RPW) ? t : 0.f;
+    }
+    xl[m] = live ? v : 0.f;
+  }
+  constexpr int RB = RPW < 32 ? RPW : 32;
+  constexpr int NB = RPW / RB;
+  const rsrc_t wr = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
+  const uint32_t voff = (uint32_t)pack_c * 4u;
+  const uint32_t row_bytes = (uint32_t)np * 4u;
+  uint32_t w[2][RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) w[0][r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + r) * row_bytes);
+
+  // ---- accumulate sum_k x * q ---------------------------------------------------
+  float part[MT][8];
+#pragma unroll
+  for (int m = 0; m < MT; ++m)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) part[m][c] = 0.f;
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b + 1 < NB) {
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        w[(b + 1) & 1][r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + (b + 1) * RB + r) * row_bytes);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if constexpr (MT >= 4) {
+        // Many rows: widen each nibble once (v_cvt_f32_f16 of the same
+        // denormal halves, half rate) and reuse it in MT full-rate FMAs,
+        // instead of MT half-rate v_fma_mix_f32 per weight.
+        float v[8];
+        word_values(w[b & 1][r], v);
+        // Opaque: otherwise the widening is folded back into v_fma_mix_f32.
+#pragma unroll
+        for (int c = 0; c < 8; ++c) asm("" : "+v"(v[c]));
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          const float xv = load_x<XT>(a.x, xrow[m] + b * RB + r);
+#pragma unroll
+          for (int c = 0; c < 8; ++c) part[m][c] = fmaf(xv, v[c], part[m][c]);
+        }
+      } else {
+        uint32_t mk[4];
+        split_word(w[b & 1][r], mk);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+          fma_word(part[m], load_x<XT>(a.x, xrow[m] + b * RB + r), mk);
+        }
+      }
+    }
+  }
+
+  // ---- fold zero point and scale (zero points in the weights' scaled domain) ----
+  float zl[8], sl[8];
+  word_values(zw, zl);
+  scales_to_f32(sraw, a.st, sl);
+  float acc[MT][8];
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    // Waves past K read row 0 and contribute nothing (uniform, once per wave).
+    if (!live) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) part[m][c] = 0.f;
+    }
+    const float xs = wave_sum(xl[m]);  // sum of x over the wave's rows
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+      acc[m][c] = sl[c] * fmaf(-zl[c], xs, part[m][c]) * col_unscale(c);
+  }
+
+  // ---- sum the waves of the workgroup (fixed order) ------------------------------
+#pragma unroll
+  for (int m = 0; m < MT; ++m) {
+    float4* dst = reinterpret_cast<float4*>(&red[wave][m][lane * 8]);
+    dst[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
+    dst[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);
+  }
+  __syncthreads();
+  constexpr int kOut = MT * kChunkCols;
+  constexpr int kPer = (kOut + 64 * WAVES - 1) / (64 * WAVES);
+  float res[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = threadIdx.x + i * 64 * WAVES;
+    float v = 0.f;
+    if (o < kOut) {
+      const int m = o / kChunkCols, c = o % kChunkCols;
+#pragma unroll
+      for (int ww = 0; ww < WAVES; ++ww) v += red[ww][m][c];
+    }
+    res[i] = v;
+  }
+
+  const int col_base = chunk * kChunkCols;
+  if (a.splits > 1) {
+    // Cross-workgroup handshake without an L2 writeback/invalidate: partials
+    // are written with agent-scope (write-through, sc1) stores, the wave waits
+    // for their completion (vmcnt 0), and only then the workgroup's arrival is
+    // counted. The last workgroup to arrive for this chunk reads all partials
+    // with agent-scope (sc1) loads, sums them in split order, and re-arms the
+    // counter for the next call.
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int o = threadIdx.x + i * 64 * WAVES;
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      if (o < kOut && m < rows && col_base + c < a.N)
+        __hip_atomic_store(&a.partial[((int64_t)split * MT + m) * a.N + col_base + c], res[i],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCounterStride], 1u,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int o = threadIdx.x + i * 64 * WAVES;
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      if (o < kOut && m < rows && col_base + c < a.N) {
+        const float* src = a.partial + (int64_t)m * a.N + col_base + c;
+        const int64_t stride = (int64_t)MT * a.N;
+        float v = 0.f;
+        int s = 0;
+        for (; s + 8 <= a.splits; s += 8) {  // 8 loads in flight, summed in split order
+          float t[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            t[j] = __hip_atomic_load(src + (s + j) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v += t[j];
+        }
+        for (; s < a.splits; ++s)
+          v += __hip_atomic_load(src + s * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res[i] = v;
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = threadIdx.x + i * 64 * WAVES;
+    const int m = o / kChunkCols, c = o % kChunkCols;
+    const int n = col_base + c;
+    if (o < kOut && m < rows && n < a.N) {
+      float v = res[i];
+      if (a.bias) v += load_f32_any(a.bias, n, a.bt);
+      store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, v);
+    }
+  }
+}
+
+int env_int(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : dflt;
+}
+
+template <int XT, int MT, int WAVES, int RPW>
+void launch_cfg(const GemmProblem& p) {
+  const int np = (int)(p.N / 8);
+  const int chunks = (np + 63) / 64;
+  const int rows_per_wg = WAVES * RPW;
+  const int splits = (int)((p.K + rows_per_wg - 1) / rows_per_wg);
+
+  GemvArgs a{};
+  a.x = p.x;
+  a.qweight = p.qweight;
+  a.qzeros = p.qzeros;
+  a.scales = p.scales;
+  a.bias = p.bias;
+  a.y = p.y;
+  a.st = p.st;
+  a.bt = p.bt;
+  a.yt = p.yt;
+  a.rows = (int32_t)p.rows;
+  a.K = (int32_t)p.K;
+  a.N = (int32_t)p.N;
+  a.group = (int32_t)p.group;
+  a.splits = splits;
+  if (splits > 1) {
+    const size_t part_bytes = (size_t)splits * MT * p.N * sizeof(float);
+    const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
+    a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
+    a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
+  }
+  hipLaunchKernelGGL((gemv_kernel<XT, MT, WAVES, RPW>), dim3(chunks, splits), dim3(64 * WAVES), 0,
+                     p.stream, a);
+  check_hip(hipGetLastError(), "gemv kernel launch");
+}
+
+// Rows per wave (a multiple of 4 dividing the group size, <= 128) and waves per
+// workgroup: enough workgroups to occupy the CUs (>= 192) with as few K splits
+// as possible, since each split adds a partial round trip at the end.
+template <int XT, int MT, int WMAX>
+void launch_rpw(const GemmProblem& p) {
+  const int g = (int)p.group;
+  const int chunks = (int)((p.N / 8 + 63) / 64);
+  int rpw = g % 32 == 0 ? 32 : g % 16 == 0 ? 16 : g % 8 == 0 ? 8 : 4;
+  if (MT >= 4 && rpw > 16) rpw = 16;  // register budget of the many-row variants
+  int waves = WMAX;
+  auto wgs = [&](int w, int r) {
+    return (int64_t)chunks * ((p.K + (int64_t)w * r - 1) / ((int64_t)w * r));
+  };
+  while (waves > 4 && wgs(waves, rpw) < 192) waves >>= 1;
+  // Long runs per wave (fewer splits) while the workgroup count stays high.
+  while (MT <= 2 && rpw < 128 && g % (2 * rpw) == 0 && wgs(waves, 2 * rpw) >= 192) rpw *= 2;
+  if (int v = env_int("AWQ_GEMV_WAVES", 0); v == 4 || v == 8 || v == 16) waves = v > WMAX ? WMAX : v;
+  if (int v = env_int("AWQ_GEMV_RPW", 0); v >= 4 && v <= 128 && g % v == 0 &&
+                                          (v == 4 || v == 8 || v == 16 || v % 32 == 0))
+    rpw = v;
+#define AWQ_GEMV_CASE(W, R) \
+  if (waves == W && rpw == R) return launch_cfg<XT, MT, W, R>(p);
+#define AWQ_GEMV_WCASES(W) \
+  AWQ_GEMV_CASE(W, 4) AWQ_GEMV_CASE(W, 8) AWQ_GEMV_CASE(W, 16) AWQ_GEMV_CASE(W, 32)
+  if constexpr (WMAX >= 16) {
+    AWQ_GEMV_WCASES(16)
+    if constexpr (MT <= 2) { AWQ_GEMV_CASE(16, 64) AWQ_GEMV_CASE(16, 96) AWQ_GEMV_CASE(16, 128) }
+  }
+  AWQ_GEMV_WCASES(8)
+  AWQ_GEMV_WCASES(4)
+  if constexpr (MT <= 2) {
+    AWQ_GEMV_CASE(8, 64) AWQ_GEMV_CASE(8, 96) AWQ_GEMV_CASE(8, 128)
+    AWQ_GEMV_CASE(4, 64) AWQ_GEMV_CASE(4, 96) AWQ_GEMV_CASE(4, 128)
+  }
+#undef AWQ_GEMV_WCASES
+#undef AWQ_GEMV_CASE
+  panic("decode GEMV: no kernel configuration for this shape");
+}
+
+template <int XT>
+void launch_xt(const GemmProblem& p) {
+  if (p.rows <= 1) launch_rpw<XT, 1, 16>(p);
+  else if (p.rows <= 2) launch_rpw<XT, 2, 16>(p);
+  else if (p.rows <= 4) launch_rpw<XT, 4, 8>(p);
+  else launch_rpw<XT, 8, 8>(p);
+}
+
+}  // namespace
+
+void launch_gemv(const GemmProblem& p) {
+  AWQ_ASSERT(p.K < (1ll << 31) && p.N < (1ll << 31) && p.K * (p.N / 8) < (1ll << 30),
+             "decode GEMV: tensor too large");
+  switch (p.xt) {
+    case AWQ_F32: launch_xt<AWQ_F32>(p); break;
+    case AWQ_F16: launch_xt<AWQ_F16>(p); break;
+    default: launch_xt<AWQ_BF16>(p); break;
+  }
+}
+
+}  // namespace cube_awq

@@ -1,0 +1,172 @@
+"""Module-level interface, mirroring the reference's `cube_awq::modules`.
+
+  AWQGEMMLinearConfig / AWQGEMMLinear   src/modules/awq_gemm.rs:54-233
+  AWQLinearConfig / AWQLinear           src/modules/awq_dequantize.rs:9-109
+
+Same constructors, builder methods, parameter shapes, `group_size()`,
+`forward()` / `dequantize()` and panic texts. Differences, all deliberate:
+  * AWQGEMMLinear.forward fuses the bias add into the kernel's epilogue (the
+    reference launches a separate elementwise add, src/modules/awq_gemm.rs:225-228).
+  * M is a runtime argument of one compiled kernel; the reference JIT-compiles
+    a kernel per distinct M (M is part of its comptime ShapeConfig).
+  * AWQLinear.forward's matmul half is the third-party GEMM of the framework
+    holding the tensors (torch here, Burn's autotuned matmul in the
+    reference, src/modules/awq_dequantize.rs:99-105).
+Parameters are plain torch tensors on the module's device: qweight/qzeros
+int32 (AutoAWQ checkpoints store int32; uint32 is accepted too), scales and
+bias in the backend float type.
+"""
+import torch
+
+from . import _lib
+from ._lib import Panic, check, lib, stream_ptr
+from .kernel import dequantize_awq
+
+AWQ_PACK_FACTOR = 8
+TILE_N_BASE = 32
+INNER_K = 64
+
+
+def _assert_eq(left, right, msg):
+    if left != right:
+        raise Panic(f"assertion `left == right` failed: {msg}\n  left: {left}\n right: {right}")
+
+
+class AWQGEMMLinearConfig:
+    def __init__(self, d_input, d_output, group_size):
+        self.d_input = d_input
+        self.d_output = d_output
+        self.group_size = group_size
+        self.bias = False
+
+    @classmethod
+    def new(cls, d_input, d_output, group_size):
+        return cls(d_input, d_output, group_size)
+
+    def with_bias(self, bias):
+        self.bias = bool(bias)
+        return self
+
+    def build(self, device=None, dtype=torch.float32):
+        """Allocates uninitialised qweight [K, N/8], qzeros [K/g, N/8], scales
+        [K/g, N] and a zero bias [N] (src/modules/awq_gemm.rs:77-124)."""
+        if not self.group_size > 0:
+            raise Panic("group_size must be > 0")
+        if self.d_output % AWQ_PACK_FACTOR != 0:
+            raise Panic(f"d_output must be divisible by {AWQ_PACK_FACTOR}")
+        if self.d_output % TILE_N_BASE != 0:
+            raise Panic(f"d_output must be divisible by TILE_N ({TILE_N_BASE})")
+        if self.d_input % INNER_K != 0:
+            raise Panic(f"d_input must be divisible by INNER_K ({INNER_K})")
+        if self.d_input % self.group_size != 0:
+            raise Panic("d_input must be divisible by group_size")
+        n_packed = self.d_output // AWQ_PACK_FACTOR
+        groups = self.d_input // self.group_size
+        qweight = torch.empty((self.d_input, n_packed), dtype=torch.int32, device=device)
+        qzeros = torch.empty((groups, n_packed), dtype=torch.int32, device=device)
+        scales = torch.empty((groups, self.d_output), dtype=dtype, device=device)
+        bias = torch.zeros((self.d_output,), dtype=dtype, device=device) if self.bias else None
+        return AWQGEMMLinear(qweight, qzeros, scales, bias)
+
+
+class AWQGEMMLinear:
+    def __init__(self, qweight, qzeros, scales, bias=None):
+        self.qweight = qweight
+        self.qzeros = qzeros
+        self.scales = scales
+        self.bias = bias
+
+    def group_size(self):
+        return self.qweight.shape[0] // self.scales.shape[0]
+
+    def forward(self, input, stream=None):
+        """input [..., K] (D >= 2) -> [..., N], fused dequant-GEMM (+ bias).
+        src/modules/awq_gemm.rs:146-232."""
+        if input.dim() < 2:
+            raise Panic("input tensor must have at least 2 dims: [..., K]")
+        dims = list(input.shape)
+        k = dims[-1]
+        if not k > 0:
+            raise Panic("input last dim (K) must be > 0")
+        numel = input.numel()
+        if numel % k != 0:
+            raise Panic("input elements must be divisible by K")
+        m = numel // k
+        x = input.reshape(m, k)
+        if not x.is_contiguous():
+            x = x.contiguous()
+        k_from_weight = self.qweight.shape[0]
+        n = self.qweight.shape[-1] * 8
+        group_size = self.group_size()
+        _assert_eq(k, k_from_weight, "input last dim (K) must match qweight rows")
+        if self.qweight.dtype not in (torch.int32, torch.uint32):
+            raise Panic("qweight must have i32/u32 dtype")
+        if self.qzeros.dtype not in (torch.int32, torch.uint32):
+            raise Panic("qzeros must have i32/u32 dtype")
+        out = torch.empty((m, n), dtype=input.dtype, device=input.device)
+        bias = self.bias
+        check(lib().awq_gemm(
+            x.data_ptr(), _lib.awq_dtype(x),
+            self.qweight.data_ptr(), self.qzeros.data_ptr(),
+            self.scales.data_ptr(), _lib.awq_dtype(self.scales),
+            bias.data_ptr() if bias is not None else None,
+            _lib.awq_dtype(bias) if bias is not None else _lib.AWQ_F32,
+            out.data_ptr(), _lib.awq_dtype(out),
+            m, k, n, group_size,
+            stream_ptr(stream, input.device if input.is_cuda else None)))
+        dims[-1] = n
+        return out.reshape(dims)
+
+    __call__ = forward
+
+
+class AWQLinearConfig:
+    def __init__(self, d_input, d_output, group_size):
+        self.d_input = d_input
+        self.d_output = d_output
+        self.group_size = group_size
+
+    @classmethod
+    def new(cls, d_input, d_output, group_size):
+        return cls(d_input, d_output, group_size)
+
+    def build(self, device=None, dtype=torch.float32):
+        """src/modules/awq_dequantize.rs:25-41 (stringified asserts)."""
+        if not self.d_output % 8 == 0:
+            raise Panic("assertion failed: self.d_output % 8 == 0")
+        if self.group_size == 0 or not self.d_input % self.group_size == 0:
+            raise Panic("assertion failed: self.d_input % self.group_size == 0")
+        if not self.d_output % 32 == 0:
+            raise Panic("assertion failed: self.d_output % 32 == 0")
+        d_out = self.d_output // 8
+        groups = self.d_input // self.group_size
+        return AWQLinear(
+            torch.empty((self.d_input, d_out), dtype=torch.int32, device=device),
+            torch.empty((groups, d_out), dtype=torch.int32, device=device),
+            torch.empty((groups, self.d_output), dtype=dtype, device=device))
+
+
+class AWQLinear:
+    def __init__(self, qweight, qzeros, scales):
+        self.qweight = qweight
+        self.qzeros = qzeros
+        self.scales = scales
+
+    def group_size(self):
+        return self.qweight.shape[0] // self.scales.shape[0]
+
+    def dequantize(self, stream=None):
+        """[K, N] weight in the scales' float type, sequential nibble order,
+        bit-exact (q - z) * s. src/modules/awq_dequantize.rs:62-72."""
+        return dequantize_awq(self.qweight, self.qzeros, self.scales, self.group_size(), stream)
+
+    def forward(self, input, stream=None):
+        """dequantize() then a library matmul, as src/modules/awq_dequantize.rs:74-108.
+        Like the reference (whose 2-D weight meets a D-rank input in Burn's
+        matmul), a rank other than 2 is rejected (here before any work is queued)."""
+        if input.dim() != 2:
+            raise Panic(f"RankMismatch {{ lhs: {input.dim()}, rhs: 2 }}")
+        weight = self.dequantize(stream)
+        return torch.matmul(input, weight.to(input.dtype))
+
+    __call__ = forward

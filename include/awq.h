@@ -1,0 +1,147 @@
+/*
+ * awq.h -- C ABI of libcube_awq_gfx950.so, the MI355X (gfx950) AWQ INT4
+ * dequant-GEMM / dequantize library.
+ *
+ * Every pointer named qweight/qzeros/scales/x/y/out/bias is a DEVICE pointer to
+ * caller-owned, row-major, contiguous memory. Calls are stream-ordered and
+ * asynchronous: they enqueue work on `stream` (a hipStream_t passed as void*,
+ * NULL = the legacy default stream) and never synchronise the host. No call
+ * allocates device memory except the GEMM split-K workspace described at
+ * awq_gemm_linear(), which is allocated once per (device, stream) and reused.
+ *
+ * Return value: 0 on success, a negative AWQ_ERR_* code otherwise. On error the
+ * thread-local string returned by awq_last_error() holds the message; for shape
+ * and dtype problems it is the exact assertion text the reference panics with,
+ * so a Rust wrapper can do `panic!("{}", awq_last_error())` and keep the
+ * reference's `#[should_panic(expected = ...)]` behaviour.
+ *
+ * Layout (AutoAWQ, reference README.md:60-70):
+ *   qweight [K, N/8] u32/i32 : 8 x 4-bit weights per word, one K row, 8 N columns
+ *   qzeros  [K/g, N/8] u32/i32
+ *   scales  [K/g, N]  f32/f16/bf16
+ * Nibble orders:
+ *   AWQ_ORDER_AUTOAWQ    packed lane p (bits 4p..4p+3) holds column [0,2,4,6,1,3,5,7][p]
+ *                        (reference src/kernel/awq_kernel_gemm.rs:7-30, used by the GEMM)
+ *   AWQ_ORDER_SEQUENTIAL column c is bits 4c..4c+3
+ *                        (reference src/kernel/awq_kernel.rs:8-19, used by dequantize)
+ */
+#ifndef CUBE_AWQ_AWQ_H
+#define CUBE_AWQ_AWQ_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types. F32/F16/BF16 for activations, scales, outputs and bias;
+ * U32/I32 for packed tensors. I16/I64 exist only so a caller can describe a
+ * wrongly-typed packed tensor and get the reference's rejection message. */
+typedef enum {
+  AWQ_F32 = 0,
+  AWQ_F16 = 1,
+  AWQ_BF16 = 2,
+  AWQ_U32 = 3,
+  AWQ_I32 = 4,
+  AWQ_I16 = 5,
+  AWQ_I64 = 6
+} awq_dtype;
+
+typedef enum { AWQ_ORDER_AUTOAWQ = 0, AWQ_ORDER_SEQUENTIAL = 1 } awq_order;
+
+enum {
+  AWQ_OK = 0,
+  AWQ_ERR_INVALID = -1, /* a constraint / shape / dtype assertion failed     */
+  AWQ_ERR_HIP = -2,     /* a HIP runtime call or kernel launch failed         */
+  AWQ_ERR_UNSUPPORTED = -3
+};
+
+/* Mirror of the reference's ShapeConfig (src/kernel/awq_kernel_gemm.rs:35-79).
+ * tile_m/tile_n/inner_k/line_size are validated exactly as the reference does
+ * (they decide which shapes are accepted) but do not pick the kernels' own
+ * tiling, which is internal. m_valid: rows >= m_valid are neither computed nor
+ * written. */
+typedef struct {
+  int64_t m, k, n;
+  int64_t tile_m, tile_n, inner_k;
+  int64_t line_size;
+  int64_t m_valid;
+} awq_shape_config;
+
+/* Mirror of CubeCL's TensorHandleRef as the reference's launchers read it:
+ * device pointer, row-major contiguous shape, element size in bytes, dtype. */
+typedef struct {
+  const void* data;
+  const int64_t* shape;
+  int32_t rank;
+  int32_t elem_size;
+  int32_t dtype; /* awq_dtype */
+} awq_tensor_ref;
+
+/* ShapeConfig::new(m, n, k, m_tile_size, n_tile_size, inner_k_size)
+ * (src/kernel/awq_kernel_gemm.rs:48-57; note the m, n, k argument order). */
+awq_shape_config awq_shape_config_new(int64_t m, int64_t n, int64_t k, int64_t m_tile_size,
+                                      int64_t n_tile_size, int64_t inner_k_size);
+/* ShapeConfig::new_with_valid_m (src/kernel/awq_kernel_gemm.rs:59-78). */
+awq_shape_config awq_shape_config_new_with_valid_m(int64_t m, int64_t n, int64_t k,
+                                                   int64_t m_tile_size, int64_t n_tile_size,
+                                                   int64_t inner_k_size, int64_t m_valid);
+
+/* validate_launch_params / validate_decode_launch_params
+ * (src/kernel/awq_kernel_gemm.rs:89-171). Host only; no GPU needed. */
+int awq_validate_launch_params(const awq_shape_config* shape, int64_t group_size);
+int awq_validate_decode_launch_params(const awq_shape_config* shape, int64_t group_size);
+
+/* awq_gemm_linear (src/kernel/awq_kernel_gemm.rs:626-771):
+ *   output[M, N] = input[M, K] . dequant(qweight, qzeros, scales)  (AutoAWQ order)
+ * with M = numel(input) / K. Same rank/shape assertions and messages, the same
+ * m_valid rule (:675-690) and the same decode/prefill split: M <= 8 runs the
+ * dequant-GEMV, M > 8 the MFMA GEMM. input/output dtype: F32, F16 or BF16;
+ * scales: F32, F16 or BF16 (may differ from input). F32 input computes in
+ * fp32; F16/BF16 input runs fp16/bf16 MFMA with fp32 accumulation. */
+int awq_gemm_linear(const awq_tensor_ref* input, const awq_tensor_ref* qweight,
+                    const awq_tensor_ref* qzeros, const awq_tensor_ref* scales,
+                    const awq_tensor_ref* output, const awq_shape_config* shape,
+                    int64_t group_size, void* stream);
+
+/* dequantize_native (src/kernel/awq_kernel.rs:63-111): sequential nibble order,
+ * out[k, n] = (F(q) - F(z)) * s, bit-exact. Rejects non-4-byte packed tensors
+ * and out_width % 32 != 0 with the reference's messages. */
+int awq_dequantize_native(const awq_tensor_ref* q_weight, const awq_tensor_ref* q_zeros,
+                          const awq_tensor_ref* q_scales, const awq_tensor_ref* output,
+                          int64_t group_size, void* stream);
+
+/* Pointer-level fused linear with the module's constraints
+ * (AWQGEMMLinear::forward, src/modules/awq_gemm.rs:146-232): tile_m/tile_n
+ * picked by awq_select_tile_m/n, INNER_K = 64, so K % 64, N % 32, g % 64,
+ * g >= 64. bias (nullable, [N], dtype b_t) is added in the epilogue before the
+ * cast to y_t; the reference adds it afterwards as a separate op (:225-228). */
+int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+             const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+             int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream);
+
+/* Pointer-level dequantize: out[K, N] in o_t from scales in s_t (s_t == o_t is
+ * the reference's single-F case), either nibble order. N % 32 == 0, K % g == 0. */
+int awq_dequantize(const uint32_t* qweight, const uint32_t* qzeros, const void* scales,
+                   int32_t s_t, void* out, int32_t o_t, int64_t K, int64_t N,
+                   int64_t group_size, int32_t order, void* stream);
+
+/* select_tile_m / select_tile_n (src/modules/awq_gemm.rs:30-52), including the
+ * AWQ_GEMM_FORCE_TILE_M environment override (:20-28). */
+int64_t awq_select_tile_m(int64_t m);
+int64_t awq_select_tile_n(int64_t n);
+
+/* DECODE_M_THRESHOLD (src/kernel/awq_kernel_gemm.rs:81): M <= this runs the GEMV. */
+int64_t awq_decode_m_threshold(void);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* awq_last_error(void);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int32_t awq_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CUBE_AWQ_AWQ_H */

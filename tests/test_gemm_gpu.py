@@ -1,0 +1,276 @@
+"""Fused AWQ dequant-GEMM on the GPU vs the oracle.
+
+Tolerances (relative L2 against the oracle's f64 sum of the reference's f32
+dequantised weights):
+  fp32 path (f32 activations, decode GEMV and fp32-MFMA prefill): 1e-5
+  fp16/bf16-MFMA prefill path:                                     2e-3
+Plus the reference's own absolute tolerances on its own cases
+(src/kernel/awq_kernel_gemm.rs:1125-1391, src/modules/awq_gemm.rs:408-604)."""
+import numpy as np
+import pytest
+import torch
+
+import awq_oracle as oracle
+import cube_awq
+from cube_awq import AWQGEMMLinear, ShapeConfig, _lib
+from conftest import load_golden
+from helpers import TORCH_OF, host_f32, make_problem, to_device, to_host
+
+pytestmark = pytest.mark.gpu
+
+TOL_FP32 = 1e-5
+TOL_MFMA = 2e-3
+AWQ_DT = {"f32": _lib.AWQ_F32, "f16": _lib.AWQ_F16, "bf16": _lib.AWQ_BF16}
+
+
+def _i32(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int32)).to(dev)
+
+
+def run_kernel(dev, x, qw, qz, sc, m, k, n, gs, tile_m=32):
+    """The reference's run_kernel (src/kernel/awq_kernel_gemm.rs:870-960):
+    ShapeConfig(rows, n, k, 32, tile_n, inner_k) through awq_gemm_linear, f32."""
+    inner_k = 64 if (k >= 64 and k % 64 == 0 and gs >= 64 and gs % 64 == 0) else 32
+    tile_n = 128 if (n >= 128 and n % 128 == 0) else 64 if (n >= 64 and n % 64 == 0) else 32
+    shape = ShapeConfig.new(m, n, k, tile_m, tile_n, inner_k)
+    out = torch.full((m, n), float("nan"), device=dev)
+    cube_awq.awq_gemm_linear(torch.from_numpy(x).to(dev), _i32(qw, dev), _i32(qz, dev),
+                             torch.from_numpy(sc).to(dev), out, shape, gs)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def uniform_word(v):
+    return int(("%x" % v) * 8, 16)
+
+
+@pytest.mark.parametrize("m,k,n,gs,w,z,s,xv,tol", [
+    (32, 32, 32, 32, 7, 0, 1.0, 0.0, 1e-5),    # kernel_zero_input_yields_zero_output
+    (32, 32, 32, 32, 5, 5, 2.0, 1.0, 1e-5),    # kernel_zero_weight_yields_zero_output
+    (32, 32, 32, 32, 15, 0, 0.0, 1.0, 1e-5),   # kernel_zero_scale_yields_zero_output
+    (32, 32, 32, 32, 5, 0, 1.0, 1.0, 1e-3),    # kernel_ones_input_uniform_weight_single_tile
+    (32, 32, 32, 32, 8, 3, 2.0, 1.0, 1e-3),    # kernel_uniform_with_nonzero_zero_point
+    (32, 32, 32, 32, 2, 7, 1.0, 1.0, 1e-3),    # kernel_negative_effective_weight
+    (32, 32, 32, 32, 15, 0, 1.0, 1.0, 1e-3),   # kernel_weight_nibble_at_max_15
+    (32, 32, 32, 32, 0, 15, 1.0, 1.0, 1e-3),   # kernel_weight_nibble_zero_zeropoint_fifteen
+    (32, 64, 32, 64, 4, 1, 1.0, 1.0, 1e-2),    # kernel_two_k_tiles
+    (32, 128, 32, 128, 6, 2, 0.25, 0.5, 1e-2), # kernel_four_k_tiles
+    (32, 64, 32, 32, 5, 1, 1.0, 1.0, 1e-2),    # kernel_two_groups_uniform_scale
+    (64, 32, 32, 32, 5, 0, 1.0, 1.0, 1e-3),    # kernel_m_double_n_single_tile
+    (1, 32, 32, 32, 5, 0, 1.0, 1.0, 1e-3),     # kernel_m_one_partial_tile
+    (32, 32, 64, 32, 3, 1, 2.0, 1.0, 1e-3),    # kernel_n_double_m_single_tile
+])
+def test_reference_kernel_uniform_cases(dev, m, k, n, gs, w, z, s, xv, tol):
+    qw = np.full((k, n // 8), uniform_word(w), np.uint32)
+    qz = np.full((k // gs, n // 8), uniform_word(z), np.uint32)
+    sc = np.full((k // gs, n), s, np.float32)
+    x = np.full((m, k), xv, np.float32)
+    out = run_kernel(dev, x, qw, qz, sc, m, k, n, gs)
+    expect = oracle.gemm_f32(x, qw, qz, sc, gs)
+    assert np.abs(out - expect).max() <= tol
+    assert np.array_equal(out, np.full((m, n), k * xv * (w - z) * s, np.float32))
+
+
+def test_reference_kernel_two_groups_different_scales(dev):
+    m, k, n, gs = 32, 64, 32, 32
+    qw = np.full((k, n // 8), uniform_word(6), np.uint32)
+    qz = np.full((k // gs, n // 8), uniform_word(2), np.uint32)
+    sc = np.concatenate([np.full((1, n), 1.0), np.full((1, n), 0.5)]).astype(np.float32)
+    out = run_kernel(dev, np.ones((m, k), np.float32), qw, qz, sc, m, k, n, gs)
+    assert np.abs(out - oracle.gemm_f32(np.ones((m, k), np.float32), qw, qz, sc, gs)).max() <= 1e-2
+
+
+def test_reference_kernel_four_groups(dev):
+    m, k, n, gs = 32, 128, 32, 32
+    qw = np.full((k, n // 8), uniform_word(7), np.uint32)
+    qz = np.full((k // gs, n // 8), uniform_word(3), np.uint32)
+    sc = np.repeat((np.arange(1, 5, dtype=np.float32) * 0.25)[:, None], n, 1)
+    x = np.ones((m, k), np.float32)
+    assert np.abs(run_kernel(dev, x, qw, qz, sc, m, k, n, gs) - oracle.gemm_f32(x, qw, qz, sc, gs)).max() <= 1e-1
+
+
+def test_reference_kernel_large_m_large_n(dev):
+    g = load_golden("gemm_large_m_large_n")
+    out = run_kernel(dev, g["x"], g["qweight"], g["qzeros"], g["scales"], 128, 32, 128, 32)
+    assert np.abs(out - g["expected"]).max() <= 1e-1
+    assert oracle.rel_l2(out, g["expected"]) <= TOL_FP32
+
+
+def test_reference_kernel_two_batches(dev):
+    # kernel_two_batches_match_cpu_ref: b=2 flattened into 64 rows.
+    m, k, n, gs = 64, 32, 32, 32
+    x = np.concatenate([np.ones((32, k)), np.full((32, k), 2.0)]).astype(np.float32)
+    qw = np.full((k, n // 8), uniform_word(5), np.uint32)
+    qz = np.full((k // gs, n // 8), uniform_word(1), np.uint32)
+    sc = np.full((k // gs, n), 0.5, np.float32)
+    out = run_kernel(dev, x, qw, qz, sc, m, k, n, gs)
+    assert np.abs(out - oracle.gemm_f32(x, qw, qz, sc, gs)).max() <= 1e-3
+
+
+@pytest.mark.parametrize("name", ["gemm_fwd_b2m32_k64n32_g32", "gemm_fwd_bias_b2m32_k64n32_g32",
+                                  "gemm_fwd_4d_1x16x14_k64n32_g32"])
+def test_module_golden_cases_through_kernel_level(dev, name):
+    # The reference module would panic on group_size 32 (it fixes INNER_K = 64);
+    # the same numbers through the kernel-level launcher with inner_k = 32.
+    g = load_golden(name)
+    x = g["x"]
+    rows, k = x.shape
+    out = run_kernel(dev, x, g["qweight"], g["qzeros"], g["scales"], rows, k, 32, 32)
+    if "bias" in g:
+        out = out + g["bias"][None, :]
+    assert np.abs(out - g["expected"]).max() <= 1e-2
+    assert oracle.rel_l2(out, g["expected"]) <= TOL_FP32
+
+
+def test_module_forward_decode_golden(dev):
+    # test_forward_decode_shape_matches_cpu_reference (src/modules/awq_gemm.rs:517-559).
+    g = load_golden("gemm_decode_b2m1_k64n32_g64")
+    layer = AWQGEMMLinear(_i32(g["qweight"], dev), _i32(g["qzeros"], dev),
+                          torch.from_numpy(g["scales"]).to(dev))
+    y = layer.forward(torch.from_numpy(g["x"]).reshape(2, 1, 64).to(dev))
+    torch.cuda.synchronize()
+    assert tuple(y.shape) == (2, 1, 32)
+    out = y.reshape(2, 32).cpu().numpy()
+    assert np.abs(out - g["expected"]).max() <= 1e-2
+    assert oracle.rel_l2(out, g["expected"]) <= TOL_FP32
+
+
+def _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, y_dt="f32", b_dt="f32", y_init=None):
+    # Keep every device tensor referenced until the launch is queued: a temporary
+    # freed before the call could be recycled by the caching allocator.
+    d_x = to_device(x, x_dt, dev)
+    d_sc = to_device(sc, s_dt, dev)
+    d_qw, d_qz = _i32(qw, dev), _i32(qz, dev)
+    d_b = to_device(b, b_dt, dev) if b is not None else None
+    y = torch.full((M, N), float("nan") if y_init is None else y_init, dtype=TORCH_OF[y_dt],
+                   device=dev)
+    _lib.check(cube_awq.lib().awq_gemm(
+        d_x.data_ptr(), AWQ_DT[x_dt], d_qw.data_ptr(), d_qz.data_ptr(),
+        d_sc.data_ptr(), AWQ_DT[s_dt], d_b.data_ptr() if d_b is not None else None, AWQ_DT[b_dt],
+        y.data_ptr(), AWQ_DT[y_dt], M, K, N, g, None))
+    torch.cuda.synchronize()
+    return y
+
+
+def _ref64(x, qw, qz, sc, b, g, x_dt, s_dt):
+    return oracle.gemm_f64(host_f32(x, x_dt), qw, qz, host_f32(sc, s_dt), g, bias=b)
+
+
+SHAPES_8B = [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)]
+
+
+@pytest.mark.parametrize("K,N", SHAPES_8B)
+@pytest.mark.parametrize("M", [1, 4, 8])
+def test_decode_sweep_fp32(dev, M, K, N):
+    # Decode sweep: f32 activations ~N(0,1), f16 scales U[0.002, 0.02], g128.
+    x, qw, qz, sc, _ = make_problem(M, K, N, 128, x_dt="f32", s_dt="f16")
+    y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, 128, "f32", "f16")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, None, 128, "f32", "f16")) <= TOL_FP32
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 6, 7])
+def test_decode_all_row_counts(dev, M):
+    K, N, g = 1024, 2080, 64  # N not a multiple of 512: partial column chunk
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f32", s_dt="f32", bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f32", "f32")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, "f32", "f32")) <= TOL_FP32
+
+
+def test_decode_config1_f32_scales(dev):
+    # M=1, 4096 -> 4096, g128, f32 activations and f32 scales (the CPU-baseline case).
+    x, qw, qz, sc, _ = make_problem(1, 4096, 4096, 128, x_dt="f32", s_dt="f32")
+    y = _gemm_ptr(dev, x, qw, qz, sc, None, 1, 4096, 4096, 128, "f32", "f32")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, None, 128, "f32", "f32")) <= TOL_FP32
+
+
+@pytest.mark.parametrize("x_dt,s_dt,y_dt", [("f16", "f16", "f16"), ("bf16", "bf16", "bf16"),
+                                             ("f16", "f32", "f32"), ("bf16", "f16", "f32")])
+def test_decode_low_precision_io(dev, x_dt, s_dt, y_dt):
+    # Decode computes in fp32 whatever the I/O types; only the output cast rounds.
+    M, K, N, g = 3, 4096, 1024, 128
+    x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt)
+    y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, x_dt, s_dt, y_dt)
+    tol = TOL_FP32 if y_dt == "f32" else (1e-3 if y_dt == "f16" else 5e-3)
+    got = host_f32(to_host(y), y_dt)
+    assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, None, g, x_dt, s_dt)) <= tol
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 14336), (14336, 4096)])
+@pytest.mark.parametrize("M", [64, 512])
+def test_prefill_sweep_f16(dev, M, K, N):
+    x, qw, qz, sc, _ = make_problem(M, K, N, 128, x_dt="f16", s_dt="f16")
+    y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, 128, "f16", "f16", "f16")
+    got = host_f32(to_host(y), "f16")
+    assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, None, 128, "f16", "f16")) <= TOL_MFMA
+
+
+def test_prefill_m2048_gate_up_sampled_rows(dev):
+    # Full-size prefill (M=2048, 4096 -> 14336): checked on 48 sampled rows.
+    M, K, N, g = 2048, 4096, 14336, 128
+    x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f16", s_dt="f16")
+    y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f16", "f16", "f16")
+    rows = np.r_[0:16, 1000:1016, 2032:2048]
+    got = host_f32(to_host(y)[rows], "f16")
+    assert oracle.rel_l2(got, _ref64(x[rows], qw, qz, sc, None, g, "f16", "f16")) <= TOL_MFMA
+
+
+@pytest.mark.parametrize("M,K,N,g", [(9, 256, 96, 64), (100, 512, 224, 128), (130, 4096, 1024, 128),
+                                     (37, 96, 64, 32), (64, 36, 32, 4)])
+@pytest.mark.parametrize("x_dt", ["f16", "bf16", "f32"])
+def test_prefill_odd_shapes(dev, M, K, N, g, x_dt):
+    s_dt = "f32" if x_dt == "f32" else x_dt
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, "f32") if K % 64 == 0 and g % 64 == 0 \
+        else None
+    if y is None:  # K or g below the module's INNER_K: kernel-level launcher, inner_k 4/32
+        inner_k = 32 if (K % 32 == 0 and g % 32 == 0) else 4
+        shape = ShapeConfig.new(M, N, K, 32, 32, inner_k)
+        y = torch.full((M, N), float("nan"), device=dev)
+        cube_awq.awq_gemm_linear(to_device(x, x_dt, dev), _i32(qw, dev), _i32(qz, dev),
+                                 to_device(sc, s_dt, dev), y, shape, g)
+        torch.cuda.synchronize()
+        ref = _ref64(x, qw, qz, sc, None, g, x_dt, s_dt)
+    else:
+        ref = _ref64(x, qw, qz, sc, b, g, x_dt, s_dt)
+    tol = TOL_FP32 if x_dt == "f32" else TOL_MFMA
+    assert oracle.rel_l2(to_host(y), ref) <= tol
+
+
+def test_m_valid_rows_untouched(dev):
+    # Rows >= m_valid are neither computed nor written (src/kernel/awq_kernel_gemm.rs:225-226).
+    for M, mv in ((40, 17), (6, 2)):
+        K, N, g = 256, 64, 64
+        x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f32", s_dt="f32")
+        y = torch.full((M, N), 123.0, device=dev)
+        shape = ShapeConfig.new_with_valid_m(M, N, K, 32, 64, 64, mv)
+        cube_awq.awq_gemm_linear(torch.from_numpy(x).to(dev), _i32(qw, dev), _i32(qz, dev),
+                                 torch.from_numpy(sc).to(dev), y, shape, g)
+        torch.cuda.synchronize()
+        out = y.cpu().numpy()
+        assert np.all(out[mv:] == 123.0)
+        assert oracle.rel_l2(out[:mv], _ref64(x[:mv], qw, qz, sc, None, g, "f32", "f32")) <= TOL_FP32
+
+
+def test_m_valid_batched_rule(dev):
+    # shape.m = 2, input flattened to 6 rows, m_valid == m -> all 6 rows valid (:675-690).
+    K, N, g = 128, 32, 64
+    x, qw, qz, sc, _ = make_problem(6, K, N, g, x_dt="f32", s_dt="f32")
+    y = torch.full((3, 2, N), 7.0, device=dev)
+    shape = ShapeConfig.new(2, N, K, 8, 32, 64)
+    cube_awq.awq_gemm_linear(torch.from_numpy(x).reshape(3, 2, K).to(dev), _i32(qw, dev),
+                             _i32(qz, dev), torch.from_numpy(sc).to(dev), y, shape, g)
+    torch.cuda.synchronize()
+    out = y.reshape(6, N).cpu().numpy()
+    assert oracle.rel_l2(out, _ref64(x, qw, qz, sc, None, g, "f32", "f32")) <= TOL_FP32
+
+
+@pytest.mark.parametrize("M", [1, 8, 256])
+def test_repeated_calls_bit_identical(dev, M):
+    # Deterministic reductions (no atomics in the sums), split-K counters reset.
+    K, N, g = 4096, 4096, 128
+    x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f16" if M > 8 else "f32", s_dt="f16")
+    x_dt = "f16" if M > 8 else "f32"
+    a = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, x_dt, "f16"))
+    for _ in range(3):
+        b = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, x_dt, "f16"))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
