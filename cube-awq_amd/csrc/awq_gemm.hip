@@ -9,14 +9,18 @@
 //   f32  activations: v_mfma_f32_32x32x2_f32, W dequantised in f32 exactly as
 //                     the reference's F = f32 kernel does
 //
-// Tiling: a 256-thread workgroup (4 waves as 2 x 2) owns a 128 x 128 tile of Y
-// and walks K in 64-row stages. Per stage it loads the X tile (row-major) and
-// the packed 64 x 16-word W tile, dequantises W in registers and writes it to
-// LDS transposed, n-major with k contiguous, so that both MFMA operands are
-// single 16-byte LDS reads (lane l of a 32x32xK MFMA needs 8 consecutive k of
-// one row of X and of one column of W). LDS is double buffered: global loads
-// of stage s+1 are in flight while stage s feeds the matrix cores, one
-// barrier per stage.
+// Tiling (template BM x BN, 2*BN threads): a workgroup of WGM x WGN waves owns
+// a BM x BN tile of Y (each wave a (BM/WGM) x (BN/WGN) block of 32 x 32 MFMA
+// tiles) and walks K in 64-row stages. Per stage it loads the X tile
+// (row-major) and the packed 64 x BN/8-word W tile, dequantises W in
+// registers (each thread 4 rows x 8 columns) and writes it to LDS transposed,
+// n-major with k contiguous, so that both MFMA operands are single 16-byte
+// LDS reads (lane l of a 32x32xK MFMA needs 8 consecutive k of one row of X
+// and of one column of W). LDS is double buffered: global loads of stage s+1
+// are in flight while stage s feeds the matrix cores, one barrier per stage.
+// Configurations: 256x256 (8 waves, 147 KB LDS, one workgroup per CU) for
+// large problems; 128x128 (4 waves) for small ones and the fp32 path. Tile
+// indices are mapped so that the tiles one XCD runs share W columns.
 //
 // f16 dequant (2.25 VALU ops per weight): for column c (packed lane L) and
 // rows r, r+1, one v_perm_b32 gathers the byte holding lane L of both words
@@ -25,6 +29,7 @@
 // v_pk_mul_f16 applies the scale: the result is the correctly rounded f16 of
 // (q - z) * s, the value the reference computes with F = f16. Odd packed
 // lanes (high nibble of the byte) take one extra shift.
+#include <cstdlib>
 #include <type_traits>
 
 #include "awq_common.h"
@@ -32,8 +37,7 @@
 namespace cube_awq {
 namespace {
 
-constexpr int kBM = 128, kBN = 128, kBK = 64;
-constexpr int kThreads = 256;
+constexpr int kBK = 64;
 
 enum { MODE_F16 = 0, MODE_BF16 = 1, MODE_F32 = 2 };
 
@@ -55,6 +59,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef f16_t f16x8 __attribute__((ext_vector_type(8)));
 typedef bf16_t bf16x8 __attribute__((ext_vector_type(8)));
 typedef f16_t f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 struct GemmArgs {
   const void* x;
@@ -65,15 +71,9 @@ struct GemmArgs {
   void* y;
   int32_t st, bt, yt;
   int32_t M, K, N, group;
-  int32_t tiles_n;
-};
-
-template <int MODE>
-struct Smem {
-  typedef typename ModeT<MODE>::T T;
-  static constexpr int kPitch = kBK + ModeT<MODE>::kPad;  // elements per LDS row
-  T a[2][kBM][kPitch];  // X tile, row-major
-  T b[2][kBN][kPitch];  // W tile, n-major (k contiguous)
+  int32_t tiles_m, tiles_n;
+  int32_t swizzled_tiles;  // leading tiles covered by the XCD mapping (multiple of 8)
+  int32_t grp_shift;       // large-tile kernel: group = 64 << grp_shift
 };
 
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -96,62 +96,94 @@ __device__ __forceinline__ uint32_t deq_pair_f16(uint32_t w0, uint32_t w1, uint3
   return __builtin_bit_cast(uint32_t, r);
 }
 
-template <int MODE, int ST>
-__global__ __launch_bounds__(kThreads, (MODE == MODE_F32) ? 1 : 2) void gemm_kernel(GemmArgs a) {
+template <int MODE, int BM, int BN, int WGM, int WGN>
+struct Tile {
   typedef typename ModeT<MODE>::T T;
+  static constexpr int kThreads = 64 * WGM * WGN;
+  static constexpr int kPitch = kBK + ModeT<MODE>::kPad;  // elements per LDS row
+  static constexpr int kWTM = BM / WGM, kWTN = BN / WGN;  // wave tile
+  static constexpr int kI = kWTM / 32, kJ = kWTN / 32;    // 32 x 32 blocks per wave
+  static constexpr int kXVec = 16 / (int)sizeof(T);       // elements per 16-byte load
+  static constexpr int kXChunksPerRow = kBK / kXVec;
+  static constexpr int kXLoads = BM * kXChunksPerRow / kThreads;
+  static constexpr size_t kSmem = (size_t)2 * (BM + BN) * kPitch * sizeof(T);
+  static_assert(kThreads == 2 * BN, "W tile mapping: each thread dequantises 4 rows x 8 columns");
+  static_assert(kWTM % 32 == 0 && kWTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+  static_assert((BM * kXChunksPerRow) % kThreads == 0, "X tile must split evenly");
+};
+
+// Hint for the register allocator: the 256x256 tile runs one workgroup per CU.
+constexpr int min_blocks(int tile_elems) { return tile_elems >= 256 * 256 ? 1 : 2; }
+
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kernel(GemmArgs a) {
+  using C = Tile<MODE, BM, BN, WGM, WGN>;
+  typedef typename C::T T;
   using S = typename Elem<ST>::type;
+  constexpr int P = C::kPitch;
   extern __shared__ __align__(16) unsigned char smem_raw[];
-  Smem<MODE>& sm = *reinterpret_cast<Smem<MODE>*>(smem_raw);
+  T* sa = reinterpret_cast<T*>(smem_raw);                 // [2][BM][P]
+  T* sb = sa + 2 * BM * P;                                // [2][BN][P]
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;  // wave position in the 2 x 2 grid
-  const int tile_m = blockIdx.x / a.tiles_n;
-  const int tile_n = blockIdx.x - tile_m * a.tiles_n;
-  const int m0 = tile_m * kBM, n0 = tile_n * kBN;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  // Tile index: consecutive workgroups are dispatched to different XCDs, so
+  // remap them to give each XCD a contiguous run of tiles (tile_m fastest:
+  // the run shares a few columns of W and so hits that XCD's L2).
+  int t = blockIdx.x;
+  if (t < a.swizzled_tiles) {
+    const int per_xcd = a.swizzled_tiles >> 3;
+    t = (t & 7) * per_xcd + (t >> 3);
+  }
+  const int tile_m = t % a.tiles_m;
+  const int tile_n = t / a.tiles_m;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int np = a.N >> 3;
   const int stages = (a.K + kBK - 1) / kBK;
 
-  // ---- per-thread load assignment -----------------------------------------
-  // X tile: kBM rows x kBK elements; thread t covers row t/2, half (t%2).
-  constexpr int kXElems = kBK / 2;                          // elements per thread
-  constexpr int kXVec = 16 / (int)sizeof(T);                // elements per 16 B
-  constexpr int kXLoads = kXElems / kXVec;                  // 16 B loads per thread
+  // ---- X tile loads: 16-byte chunks, chunk c = tid + i*T: row c/8, k 8*(c%8)
   using XIn = typename std::conditional<MODE == MODE_F32, float, T>::type;
-  const int xr = tid >> 1;
-  const int xk = (tid & 1) * kXElems;
-  const bool x_row_ok = (m0 + xr) < a.M;
-  const XIn* xsrc = static_cast<const XIn*>(a.x) + (int64_t)(x_row_ok ? m0 + xr : 0) * a.K + xk;
+  constexpr int XV = C::kXVec;
+  const XIn* xsrc[C::kXLoads];
+  int xrow[C::kXLoads], xk[C::kXLoads];
+  bool xrow_ok[C::kXLoads];
+#pragma unroll
+  for (int i = 0; i < C::kXLoads; ++i) {
+    const int c = tid + i * C::kThreads;
+    xrow[i] = c / C::kXChunksPerRow;
+    xk[i] = (c % C::kXChunksPerRow) * XV;
+    xrow_ok[i] = (m0 + xrow[i]) < a.M;
+    xsrc[i] = static_cast<const XIn*>(a.x) + (int64_t)(xrow_ok[i] ? m0 + xrow[i] : 0) * a.K + xk[i];
+  }
+  // 16-byte X loads need 16-byte aligned rows: K a multiple of the vector.
+  const bool x_vec = (a.K % XV) == 0;
 
-  // W tile: 16 packed words per row x 64 rows; thread t covers word t%16 of
-  // rows 4*(t/16) .. +3.
-  const int wp = tid & 15;
-  const int wq = tid >> 4;
+  // ---- W tile: thread covers packed word wp of rows 4*wq .. 4*wq+3
+  const int wp = tid % (BN / 8);
+  const int wq = tid / (BN / 8);
   const int pack = (n0 >> 3) + wp;
   const bool w_ok = pack < np;
   const uint32_t* wsrc = a.qweight + (w_ok ? pack : 0);
 
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 xreg[kXLoads];
+  u32x4 xreg[C::kXLoads];
   uint32_t wreg[4];
-
-  // 16-byte X loads need 16-byte aligned rows: K a multiple of the vector.
-  const bool x_vec = (a.K % kXVec) == 0;
 
   auto load_stage = [&](int s) {
     const int k0 = s * kBK;
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i) {
-      const int k = k0 + xk + i * kXVec;
-      if (x_row_ok && x_vec && k + kXVec <= a.K) {
-        xreg[i] = *reinterpret_cast<const u32x4*>(xsrc + k0 + i * kXVec);
-      } else if (x_row_ok && k < a.K) {
+    for (int i = 0; i < C::kXLoads; ++i) {
+      const int k = k0 + xk[i];
+      if (xrow_ok[i] && x_vec && k + XV <= a.K) {
+        xreg[i] = *reinterpret_cast<const u32x4*>(xsrc[i] + k0);
+      } else if (xrow_ok[i] && k < a.K) {
         // K is a multiple of 4 only: the last vector of a row may be partial.
-        typedef XIn xv_t __attribute__((ext_vector_type(kXVec)));
+        typedef XIn xv_t __attribute__((ext_vector_type(XV)));
         xv_t v;
 #pragma unroll
-        for (int e = 0; e < kXVec; ++e) v[e] = (k + e < a.K) ? xsrc[k0 + i * kXVec + e] : (XIn)0.0f;
+        for (int e = 0; e < XV; ++e) v[e] = (k + e < a.K) ? xsrc[i][k0 + e] : (XIn)0.0f;
         xreg[i] = __builtin_bit_cast(u32x4, v);
       } else {
         xreg[i] = u32x4{0u, 0u, 0u, 0u};
@@ -167,17 +199,16 @@ __global__ __launch_bounds__(kThreads, (MODE == MODE_F32) ? 1 : 2) void gemm_ker
   auto store_stage = [&](int s, int buf) {
     // X: straight copy into row-major LDS.
 #pragma unroll
-    for (int i = 0; i < kXLoads; ++i)
-      *reinterpret_cast<u32x4*>(&sm.a[buf][xr][xk + i * kXVec]) = xreg[i];
+    for (int i = 0; i < C::kXLoads; ++i)
+      *reinterpret_cast<u32x4*>(&sa[(buf * BM + xrow[i]) * P + xk[i]]) = xreg[i];
     // W: dequantise 4 rows x 8 columns, write k-contiguous per column.
+    T* bdst = &sb[(buf * BN + wp * 8) * P + wq * 4];
     const int k0 = s * kBK + wq * 4;
     if (!w_ok || k0 >= a.K) {
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        T* dst = &sm.b[buf][wp * 8 + c][wq * 4];
+      for (int c = 0; c < 8; ++c)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dst[r] = (T)0.0f;
-      }
+        for (int r = 0; r < 4; ++r) bdst[c * P + r] = (T)0.0f;
       return;
     }
     const int grp = k0 / a.group;
@@ -185,25 +216,23 @@ __global__ __launch_bounds__(kThreads, (MODE == MODE_F32) ? 1 : 2) void gemm_ker
     const S* srow = static_cast<const S*>(a.scales) + (int64_t)grp * a.N + (int64_t)pack * 8;
     if constexpr (MODE == MODE_F16) {
       uint32_t out[8][2];
-#define AWQ_DEQ_COL(C)                                                                 \
+#define AWQ_DEQ_COL(CC)                                                                \
   {                                                                                     \
-    constexpr int L = awq_lane_of_col(C);                                               \
+    constexpr int L = awq_lane_of_col(CC);                                              \
     const uint32_t z = (zw >> (4 * L)) & 0xFu;                                          \
     const f16_t zf = (f16_t)(1024.0f + (float)z);                                       \
-    const f16_t sf = (f16_t)to_f32(srow[C]);                                            \
+    const f16_t sf = (f16_t)to_f32(srow[CC]);                                           \
     const uint32_t zc = (uint32_t)__builtin_bit_cast(uint16_t, zf) * 0x10001u;          \
     const uint32_t scc = (uint32_t)__builtin_bit_cast(uint16_t, sf) * 0x10001u;         \
-    out[C][0] = deq_pair_f16<L>(wreg[0], wreg[1], zc, scc);                             \
-    out[C][1] = deq_pair_f16<L>(wreg[2], wreg[3], zc, scc);                             \
+    out[CC][0] = deq_pair_f16<L>(wreg[0], wreg[1], zc, scc);                            \
+    out[CC][1] = deq_pair_f16<L>(wreg[2], wreg[3], zc, scc);                            \
   }
       AWQ_DEQ_COL(0) AWQ_DEQ_COL(1) AWQ_DEQ_COL(2) AWQ_DEQ_COL(3)
       AWQ_DEQ_COL(4) AWQ_DEQ_COL(5) AWQ_DEQ_COL(6) AWQ_DEQ_COL(7)
 #undef AWQ_DEQ_COL
 #pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        *reinterpret_cast<u32x2*>(&sm.b[buf][wp * 8 + c][wq * 4]) = u32x2{out[c][0], out[c][1]};
-      }
+      for (int c = 0; c < 8; ++c)
+        *reinterpret_cast<u32x2*>(&bdst[c * P]) = u32x2{out[c][0], out[c][1]};
     } else {
       // bf16 / f32: (float(q) - float(z)) * s in f32 (the reference's F = f32
       // arithmetic), then one rounding to T.
@@ -211,61 +240,68 @@ __global__ __launch_bounds__(kThreads, (MODE == MODE_F32) ? 1 : 2) void gemm_ker
       for (int c = 0; c < 8; ++c) {
         const int L = awq_lane_of_col(c);
         const int z = (int)((zw >> (4 * L)) & 0xFu);
-        const float s = to_f32(srow[c]);
+        const float sv = to_f32(srow[c]);
         T v[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int q = (int)((wreg[r] >> (4 * L)) & 0xFu);
-          v[r] = from_f32<T>((float)(q - z) * s);
+          v[r] = from_f32<T>((float)(q - z) * sv);
         }
-        T* dst = &sm.b[buf][wp * 8 + c][wq * 4];
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<u32x2*>(&bdst[c * P]) =
+              u32x2{(uint32_t)__builtin_bit_cast(uint16_t, v[0]) | ((uint32_t)__builtin_bit_cast(uint16_t, v[1]) << 16),
+                    (uint32_t)__builtin_bit_cast(uint16_t, v[2]) | ((uint32_t)__builtin_bit_cast(uint16_t, v[3]) << 16)};
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dst[r] = v[r];
+          for (int r = 0; r < 4; ++r) bdst[c * P + r] = v[r];
+        }
       }
     }
   };
 
-  // ---- accumulators: wave tile 64 x 64 = 2 x 2 blocks of 32 x 32 ------------
-  f32x16 acc[2][2];
+  // ---- accumulators: kI x kJ blocks of 32 x 32 per wave ------------------------
+  f32x16 acc[C::kI][C::kJ];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < C::kI; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < C::kJ; ++j) acc[i][j] = f32x16{};
 
-  const int arow = wm * 64 + (lane & 31);  // + 32*i
-  const int bcol = wn * 64 + (lane & 31);  // + 32*j
-  const int kofs = (lane >> 5);            // which half of the MFMA k-slice
+  const int arow = wm * C::kWTM + (lane & 31);  // + 32*i
+  const int bcol = wn * C::kWTN + (lane & 31);  // + 32*j
+  const int kofs = (lane >> 5);                  // which half of the MFMA k-slice
 
   auto compute_stage = [&](int buf) {
+    const T* A = sa + buf * BM * P;
+    const T* B = sb + buf * BN * P;
     if constexpr (MODE == MODE_F32) {
 #pragma unroll 4
       for (int kk = 0; kk < kBK; kk += 2) {
-        float av[2], bv[2];
+        float av[C::kI], bv[C::kJ];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) av[i] = sm.a[buf][arow + 32 * i][kk + kofs];
+        for (int i = 0; i < C::kI; ++i) av[i] = A[(arow + 32 * i) * P + kk + kofs];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) bv[j] = sm.b[buf][bcol + 32 * j][kk + kofs];
+        for (int j = 0; j < C::kJ; ++j) bv[j] = B[(bcol + 32 * j) * P + kk + kofs];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < C::kI; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j)
+          for (int j = 0; j < C::kJ; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[i], bv[j], acc[i][j], 0, 0, 0);
       }
     } else {
       typedef typename std::conditional<MODE == MODE_F16, f16x8, bf16x8>::type V8;
 #pragma unroll
       for (int kk = 0; kk < kBK; kk += 16) {
-        V8 av[2], bv[2];
+        V8 av[C::kI], bv[C::kJ];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-          av[i] = *reinterpret_cast<const V8*>(&sm.a[buf][arow + 32 * i][kk + kofs * 8]);
+        for (int i = 0; i < C::kI; ++i)
+          av[i] = *reinterpret_cast<const V8*>(&A[(arow + 32 * i) * P + kk + kofs * 8]);
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-          bv[j] = *reinterpret_cast<const V8*>(&sm.b[buf][bcol + 32 * j][kk + kofs * 8]);
+        for (int j = 0; j < C::kJ; ++j)
+          bv[j] = *reinterpret_cast<const V8*>(&B[(bcol + 32 * j) * P + kk + kofs * 8]);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < C::kI; ++i)
 #pragma unroll
-          for (int j = 0; j < 2; ++j) {
+          for (int j = 0; j < C::kJ; ++j) {
             if constexpr (MODE == MODE_F16)
               acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[i], bv[j], acc[i][j], 0, 0, 0);
             else
@@ -291,23 +327,344 @@ __global__ __launch_bounds__(kThreads, (MODE == MODE_F32) ? 1 : 2) void gemm_ker
   // ---- epilogue: D layout of a 32x32 MFMA: lane l, register r ->
   //      row 8*(r/4) + 4*(l/32) + r%4, column l%32 ----------------------------
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
+  for (int j = 0; j < C::kJ; ++j) {
     const int n = n0 + bcol + 32 * j;
     if (n >= a.N) continue;
     const float bias = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < C::kI; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][j][r] + bias);
       }
     }
   }
 }
 
-template <int MODE, int ST>
-void launch_typed(const GemmProblem& p) {
+// ===========================================================================
+// Large-tile f16/bf16 kernel: one workgroup per CU, 128 KB of LDS.
+//
+// Requirements (checked by the launcher): K % 64 == 0, group = 64 * 2^j, X
+// and W small enough for 32-bit buffer offsets. Each wave owns a (BM/WGM) x
+// (BN/WGN) block of Y in 32 x 32 MFMA tiles.
+//
+// LDS rows are 128 bytes (64 k of one row of X or one column of W) made of
+// eight 16-byte granules; granule g of row r is stored in slot g ^ swz(r).
+// The swizzle makes the MFMA operand reads (32 consecutive rows, one granule)
+// and the dequantised-W writes (rows 8 apart, one granule) bank-conflict
+// free without padding.
+//
+// Software pipeline per 64-row stage s (buffers s & 1):
+//   issue LDS-direct X loads for s+1 and packed W / zeros / scales for s+2,
+//   per 16-k slice: MFMAs of stage s, then dequantise two columns of W(s+1)
+//   (loaded a stage ago) into the other buffer; one barrier.
+// ===========================================================================
+__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+
+// Packed lane L of two words as f16x2 magic numbers: the byte holding lane L
+// of w0 and of w1 goes to the two halves (v_perm_b32), then one v_bitop3
+// keeps the nibble and ORs in the exponent: low nibble (even L) -> 0x6400 | q
+// = 1024 + q, high nibble (odd L) -> 0x5400 | q << 4 = 64 + q (mantissa unit
+// 1/16 at exponent 6). L must be a compile-time constant after inlining.
+__device__ __forceinline__ uint32_t nib_f16x2(uint32_t w0, uint32_t w1, int L) {
+  const uint32_t b = (uint32_t)L >> 1;
+  const uint32_t h = __builtin_amdgcn_perm(w1, w0, b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24));
+  return (L & 1) ? __builtin_amdgcn_bitop3_b32(h, 0x00F000F0u, 0x54005400u, 0xEA)
+                 : __builtin_amdgcn_bitop3_b32(h, 0x000F000Fu, 0x64006400u, 0xEA);
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane l's data lands at
+// dst + 16 l (dst is wave-uniform; it goes through M0).
+__device__ __forceinline__ void lds_dma16(rsrc_t r, unsigned char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+template <int MODE, int BM, int BN, int WGM, int WGN>
+struct BigTile {
+  typedef typename ModeT<MODE>::T T;
+  static constexpr int kThreads = 64 * WGM * WGN;
+  static constexpr int kRowBytes = kBK * 2;
+  static constexpr int kWTM = BM / WGM, kWTN = BN / WGN;
+  static constexpr int kI = kWTM / 32, kJ = kWTN / 32;
+  static constexpr int kPacks = BN / 8;                         // packed words per W row
+  static constexpr int kRW = (64 * kPacks / kThreads >= 8) ? 8 : 4;  // W rows per thread
+  static constexpr int kWThreads = kPacks * (kBK / kRW);
+  static constexpr int kABytes = BM * kRowBytes;  // one X buffer
+  static constexpr int kBBytes = BN * kRowBytes;  // one W buffer
+  // Layout: X buffer 0, X buffer 1, W buffer 0, W buffer 1.
+  static constexpr size_t kSmem = 2 * (size_t)(kABytes + kBBytes);
+  static_assert(MODE != MODE_F32, "large-tile kernel is f16/bf16 only");
+  static_assert(kWThreads <= kThreads, "W tile needs more threads");
+  static_assert((BM / 8) % (kThreads / 64) == 0, "X tile must split evenly over the waves");
+  static_assert(kWTM % 32 == 0 && kWTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+};
+
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a) {
+  using C = BigTile<MODE, BM, BN, WGM, WGN>;
+  using S = typename Elem<ST>::type;
+  constexpr int RW = C::kRW;
+  constexpr int kSW = (sizeof(S) * 8) / 4;  // dwords holding a pack's 8 scales
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WGN, wn = wave % WGN;
+
+  int t = blockIdx.x;
+  if (t < a.swizzled_tiles) {
+    const int per_xcd = a.swizzled_tiles >> 3;
+    t = (t & 7) * per_xcd + (t >> 3);
+  }
+  const int tile_m = t % a.tiles_m;
+  const int tile_n = t / a.tiles_m;
+  const int m0 = tile_m * BM, n0 = tile_n * BN;
+  const int np = a.N >> 3;
+  const int stages = a.K / kBK;
+
+  // ---- X: copied global -> LDS directly (buffer_load ... lds). One
+  // instruction moves 64 x 16 bytes into 1 KB of LDS, lane l landing in row
+  // l >> 3, slot l & 7 of an 8-row chunk; so lane l fetches the granule that
+  // belongs in that slot, (l & 7) ^ swz(row). Wave w fills chunks w + i*NW.
+  constexpr int NW = C::kThreads / 64;
+  constexpr int kXIns = BM / 8 / NW;
+  const rsrc_t xres = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
+  uint32_t xvoff[kXIns];
+#pragma unroll
+  for (int i = 0; i < kXIns; ++i) {
+    const int row = 8 * (wave + i * NW) + (lane >> 3);
+    const int grow = min(m0 + row, a.M - 1);  // rows past M read row M-1; never stored
+    const int gran = (lane & 7) ^ swz(row);
+    xvoff[i] = (uint32_t)(grow * a.K + gran * 8) * 2u;
+  }
+
+  // ---- W: thread covers pack wp, rows wq*RW .. wq*RW+RW-1 of each stage ----
+  const bool w_act = tid < C::kWThreads;
+  const int wp = tid % C::kPacks;
+  const int wq = w_act ? tid / C::kPacks : 0;
+  const int pack = min((n0 >> 3) + wp, np - 1);  // ragged N: clamp, never stored
+  const rsrc_t wres = make_rsrc(a.qweight, (uint32_t)((int64_t)a.K * np * 4));
+  const rsrc_t zres = make_rsrc(a.qzeros, (uint32_t)((int64_t)(a.K / a.group) * np * 4));
+  const rsrc_t sres = make_rsrc(a.scales, (uint32_t)((int64_t)(a.K / a.group) * a.N * sizeof(S)));
+  const uint32_t wvoff = (uint32_t)((wq * RW) * np + pack) * 4u;
+  const uint32_t row_bytes = (uint32_t)np * 4u;
+  // LDS byte offset (within a W buffer) of this thread's k-run in column 8 wp:
+  // swz(8 wp + c) = (c ^ wp) & 7, so column 8 wp + c uses this slot ^ c.
+  const uint32_t wl0 = (uint32_t)(wp * 8 * C::kRowBytes) +
+                       (uint32_t)((((wq * RW) >> 3) ^ (wp & 7)) << 4) + (((wq * RW) & 7) ? 8u : 0u);
+
+  // Two register sets for packed W / zeros / scales, used alternately: one
+  // being dequantised, the other in flight two stages ahead.
+  struct WRegs {
+    uint32_t w[RW];
+    uint32_t z;
+    uint32_t sv[kSW];
+  };
+  WRegs wa, wb;
+
+  auto load_w = [&](int s, WRegs& r_) {
+    const int k0 = s * kBK;
+#pragma unroll
+    for (int r = 0; r < RW; ++r) r_.w[r] = buf_load_u32_nt(wres, wvoff, (uint32_t)(k0 + r) * row_bytes);
+    const int grp = s >> a.grp_shift;  // a 64-row stage lies in one group
+    r_.z = buf_load_u32(zres, (uint32_t)(grp * np + pack) * 4u, 0);
+    const uint32_t soff = (uint32_t)(grp * a.N + pack * 8) * (uint32_t)sizeof(S);
+#pragma unroll
+    for (int v = 0; v < kSW; v += 4) {
+      const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(sres, soff + v * 4, 0, 0);
+      r_.sv[v] = q[0]; r_.sv[v + 1] = q[1]; r_.sv[v + 2] = q[2]; r_.sv[v + 3] = q[3];
+    }
+  };
+  auto scale_of = [&](const uint32_t (&sv)[kSW], int c) -> float {
+    if constexpr (sizeof(S) == 4) return __builtin_bit_cast(float, sv[c]);
+    else {
+      const uint16_t h = (uint16_t)(sv[c >> 1] >> (16 * (c & 1)));
+      return to_f32(__builtin_bit_cast(S, h));
+    }
+  };
+
+  auto load_x = [&](int s, int buf) {
+    const uint32_t koff = (uint32_t)(s * kBK) * 2u;
+#pragma unroll
+    for (int i = 0; i < kXIns; ++i) {
+      lds_dma16(xres, smem_raw + buf * C::kABytes + (wave + i * NW) * 1024, xvoff[i], koff);
+    }
+  };
+
+  // Dequantise column c of the pack (RW k values) and write it to W buffer
+  // buf: LDS column 8 wp + c, whose slot is that of column 8 wp flipped by c.
+  auto deq_store_col = [&](const WRegs& r_, int c, int buf) {
+    uint32_t dq[RW / 2];
+    const int L = awq_lane_of_col(c);
+    const uint32_t zw = r_.z;
+    if constexpr (MODE == MODE_F16) {
+      // Nibbles of packed lane L as f16 magic numbers (1024 + q or 64 + q),
+      // zero likewise; (v - zc) is exact and * sc rounds once.
+      const uint32_t zc = nib_f16x2(zw, zw, L);
+      uint32_t scc;
+      if constexpr (ST == AWQ_F16) {
+        scc = __builtin_amdgcn_perm(r_.sv[c >> 1], r_.sv[c >> 1], (c & 1) ? 0x03020302u : 0x01000100u);
+      } else {
+        const f16_t sf = (f16_t)scale_of(r_.sv, c);
+        scc = (uint32_t)__builtin_bit_cast(uint16_t, sf) * 0x10001u;
+      }
+      const f16x2 fz = __builtin_bit_cast(f16x2, zc);
+      const f16x2 fs = __builtin_bit_cast(f16x2, scc);
+#pragma unroll
+      for (int r = 0; r < RW / 2; ++r) {
+        const f16x2 fv = __builtin_bit_cast(f16x2, nib_f16x2(r_.w[2 * r], r_.w[2 * r + 1], L));
+        dq[r] = __builtin_bit_cast(uint32_t, (fv - fz) * fs);
+      }
+    } else {
+      // bf16: (q - z) * s is exact in f32 (5-bit by at most 24-bit
+      // significand); one rounding to bf16 gives the bf16 product.
+      const int z = (int)((zw >> (4 * L)) & 0xFu);
+      const float sv_ = scale_of(r_.sv, c);
+#pragma unroll
+      for (int r = 0; r < RW / 2; ++r) {
+        const int q0 = (int)((r_.w[2 * r] >> (4 * L)) & 0xFu);
+        const int q1 = (int)((r_.w[2 * r + 1] >> (4 * L)) & 0xFu);
+        const bf16_t v0 = from_f32<bf16_t>((float)(q0 - z) * sv_);
+        const bf16_t v1 = from_f32<bf16_t>((float)(q1 - z) * sv_);
+        dq[r] = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
+      }
+    }
+    if constexpr (C::kWThreads < C::kThreads) {
+      if (!w_act) return;
+    }
+    uint32_t off = wl0;
+    asm volatile("" : "+v"(off));  // recompute per use: keeps 8 addresses out of the register file
+    unsigned char* dst = smem_raw + ((off ^ (uint32_t)(c << 4)) + (uint32_t)(2 * C::kABytes + buf * C::kBBytes + c * C::kRowBytes));
+    if constexpr (RW == 8)
+      *reinterpret_cast<u32x4*>(dst) = u32x4{dq[0], dq[1], dq[2], dq[3]};
+    else
+      *reinterpret_cast<u32x2*>(dst) = u32x2{dq[0], dq[1]};
+  };
+
+  // ---- MFMA operand addressing -------------------------------------------
+  f32x16 acc[C::kI][C::kJ];
+#pragma unroll
+  for (int i = 0; i < C::kI; ++i)
+#pragma unroll
+    for (int j = 0; j < C::kJ; ++j) acc[i][j] = f32x16{};
+  const int h = lane >> 5;  // which 8-k half of the 16-k MFMA slice
+  // Row wm*WTM + 32 i + (lane & 31): its swizzle is swz(lane & 31) with bit 2
+  // flipped by (4 i + wm*WTM/8) & 4, so two base registers per operand and
+  // the 32-row step as an immediate. k-slice kq flips slot bits 1-2 (kq << 5).
+  const uint32_t lr = (uint32_t)(lane & 31);
+  const uint32_t a_base = (uint32_t)((wm * C::kWTM) * C::kRowBytes) + lr * C::kRowBytes +
+                          (uint32_t)((h ^ swz((int)lr)) << 4);
+  const uint32_t b_base = (uint32_t)(2 * C::kABytes) + (uint32_t)((wn * C::kWTN) * C::kRowBytes) +
+                          lr * C::kRowBytes + (uint32_t)((h ^ swz((int)lr)) << 4);
+  const uint32_t a_fl = (uint32_t)(((wm * (C::kWTM / 8)) & 4) << 4);
+  const uint32_t b_fl = (uint32_t)(((wn * (C::kWTN / 8)) & 4) << 4);
+  const uint32_t a_par[2] = {a_base ^ a_fl, a_base ^ a_fl ^ 64u};
+  const uint32_t b_par[2] = {b_base ^ b_fl, b_base ^ b_fl ^ 64u};
+  typedef typename std::conditional<MODE == MODE_F16, f16x8, bf16x8>::type V8;
+  typedef V8 Frags[C::kI + C::kJ];
+  auto read_frags = [&](int buf, int kq, Frags& f) {
+#pragma unroll
+    for (int i = 0; i < C::kI; ++i)
+      f[i] = *reinterpret_cast<const V8*>(smem_raw + (a_par[i & 1] ^ (uint32_t)(kq << 5)) +
+                                          (buf * C::kABytes + i * 32 * C::kRowBytes));
+#pragma unroll
+    for (int j = 0; j < C::kJ; ++j)
+      f[C::kI + j] = *reinterpret_cast<const V8*>(smem_raw + (b_par[j & 1] ^ (uint32_t)(kq << 5)) +
+                                                  (buf * C::kBBytes + j * 32 * C::kRowBytes));
+  };
+  auto mfmas = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < C::kI; ++i)
+#pragma unroll
+      for (int j = 0; j < C::kJ; ++j) {
+        if constexpr (MODE == MODE_F16)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], f[C::kI + j], acc[i][j], 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[C::kI + j], acc[i][j], 0, 0, 0);
+      }
+  };
+
+  // ---- prologue ------------------------------------------------------------
+  load_x(0, 0);
+  load_w(0, wa);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) deq_store_col(wa, c, 0);
+  load_w(min(1, stages - 1), wa);
+  __syncthreads();
+
+  // ---- main loop -----------------------------------------------------------
+  // Branch-free body: at the tail the prefetches clamp to the last stage and
+  // the writes go to the buffer nobody reads any more, so one basic block
+  // holds the loads, the dequantisation and the MFMAs for the scheduler to
+  // interleave. The barrier also waits for the LDS-direct loads (vmcnt), so
+  // W for stage s+2 lands by the end of stage s and is dequantised in s+1.
+  // Unrolled by two so the register sets alternate without copies.
+  // Instruction order inside one 16-k slice: the operand reads for the next
+  // slice first, then each MFMA followed by a few dequantisation VALU ops
+  // (they run while the matrix core is busy), then the LDS writes.
+  auto interleave = [&]() {
+    constexpr int kM = C::kI * C::kJ;
+    __builtin_amdgcn_sched_group_barrier(0x100, C::kI + C::kJ, 0);  // DS read
+#pragma unroll
+    for (int q = 0; q < kM; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+    }
+    __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);  // DS write
+  };
+  // Within a stage the operand reads for slice kq+1 are issued before the
+  // MFMAs of slice kq; scheduling fences keep each slice's reads, MFMAs and
+  // dequantisation together so the live registers stay bounded.
+  auto step = [&](int s, int buf, WRegs& deq, WRegs& next) {
+    load_x(min(s + 1, stages - 1), buf ^ 1);
+    load_w(min(s + 2, stages - 1), next);
+    Frags f0, f1;
+    read_frags(buf, 0, f0);
+#pragma unroll
+    for (int kq = 0; kq < kBK / 16; kq += 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(buf, kq + 1, f1);
+      mfmas(f0);
+      deq_store_col(deq, 2 * kq, buf ^ 1);
+      deq_store_col(deq, 2 * kq + 1, buf ^ 1);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      if (kq + 2 < kBK / 16) read_frags(buf, kq + 2, f0);
+      mfmas(f1);
+      deq_store_col(deq, 2 * kq + 2, buf ^ 1);
+      deq_store_col(deq, 2 * kq + 3, buf ^ 1);
+      interleave();
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __syncthreads();
+  };
+  for (int s = 0; s < stages; s += 2) {
+    step(s, 0, wa, wb);
+    if (s + 1 < stages) step(s + 1, 1, wb, wa);
+  }
+
+  // ---- epilogue --------------------------------------------------------------
+#pragma unroll
+  for (int j = 0; j < C::kJ; ++j) {
+    const int n = n0 + wn * C::kWTN + 32 * j + (lane & 31);
+    if (n >= a.N) continue;
+    const float bias = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
+#pragma unroll
+    for (int i = 0; i < C::kI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][j][r] + bias);
+      }
+    }
+  }
+}
+
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+void launch_big(const GemmProblem& p) {
+  using C = BigTile<MODE, BM, BN, WGM, WGN>;
   GemmArgs a{};
   a.x = p.x;
   a.qweight = p.qweight;
@@ -322,28 +679,99 @@ void launch_typed(const GemmProblem& p) {
   a.K = (int32_t)p.K;
   a.N = (int32_t)p.N;
   a.group = (int32_t)p.group;
-  const int tiles_m = (int)((p.rows + kBM - 1) / kBM);
-  const int tiles_n = (int)((p.N + kBN - 1) / kBN);
-  a.tiles_n = tiles_n;
-  const size_t smem = sizeof(Smem<MODE>);
+  a.tiles_m = (int)((p.rows + BM - 1) / BM);
+  a.tiles_n = (int)((p.N + BN - 1) / BN);
+  const int tiles = a.tiles_m * a.tiles_n;
+  a.swizzled_tiles = tiles & ~7;
+  a.grp_shift = __builtin_ctzll(p.group / kBK);
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kSmem),
+              "hipFuncSetAttribute(gemm_big)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>), dim3(tiles), dim3(C::kThreads),
+                     C::kSmem, p.stream, a);
+  check_hip(hipGetLastError(), "gemm kernel launch");
+}
+
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+void launch_cfg(const GemmProblem& p) {
+  using C = Tile<MODE, BM, BN, WGM, WGN>;
+  GemmArgs a{};
+  a.x = p.x;
+  a.qweight = p.qweight;
+  a.qzeros = p.qzeros;
+  a.scales = p.scales;
+  a.bias = p.bias;
+  a.y = p.y;
+  a.st = p.st;
+  a.bt = p.bt;
+  a.yt = p.yt;
+  a.M = (int32_t)p.rows;
+  a.K = (int32_t)p.K;
+  a.N = (int32_t)p.N;
+  a.group = (int32_t)p.group;
+  a.tiles_m = (int)((p.rows + BM - 1) / BM);
+  a.tiles_n = (int)((p.N + BN - 1) / BN);
+  const int tiles = a.tiles_m * a.tiles_n;
+  a.swizzled_tiles = tiles & ~7;
+  const size_t smem = C::kSmem;
+  static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
+  if (!attr_set) {
+    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
               "hipFuncSetAttribute(gemm)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<MODE, ST>), dim3(tiles_m * tiles_n), dim3(kThreads), smem,
-                     p.stream, a);
+  hipLaunchKernelGGL((gemm_kernel<MODE, ST, BM, BN, WGM, WGN>), dim3(tiles), dim3(C::kThreads),
+                     smem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
 
-template <int MODE>
+int env_int(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : dflt;
+}
+
+// Tile choice. f16/bf16 problems with K % 64 == 0 and group = 64 * 2^j use the
+// large-tile kernel with the largest tile that still yields a full wave of
+// workgroups; anything else (fp32, K % 64 != 0, tiny problems) the generic
+// 128x128 kernel.
+template <int MODE, int ST>
 void launch_mode(const GemmProblem& p) {
+  int cfg = env_int("AWQ_GEMM_TILE", 0);  // tuning override: 1 generic, 2.. large tiles
+  const int64_t gs = p.group / kBK;
+  const bool big_ok = MODE != MODE_F32 && p.K % kBK == 0 && p.group % kBK == 0 && (gs & (gs - 1)) == 0 &&
+                      p.rows * p.K * 2 < (1ll << 32) && p.K * (p.N / 8) * 4 < (1ll << 32) &&
+                      (p.K / p.group) * p.N * 4 < (1ll << 32);
+  if (!big_ok) cfg = 1;
+  if (cfg == 0) {
+    auto tiles = [&](int bm, int bn) { return ((p.rows + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
+    if (tiles(256, 256) >= 240) cfg = 2;
+    else if (tiles(128, 256) >= 240) cfg = 3;
+    else if (tiles(128, 128) >= 120) cfg = 4;
+    else cfg = 1;
+  }
+  if constexpr (MODE != MODE_F32) {
+    switch (cfg) {
+      case 2: return launch_big<MODE, ST, 256, 256, 2, 4>(p);
+      case 3: return launch_big<MODE, ST, 128, 256, 2, 4>(p);
+      case 4: return launch_big<MODE, ST, 128, 128, 2, 2>(p);
+      case 6: return launch_big<MODE, ST, 256, 128, 4, 2>(p);
+      default: break;
+    }
+  }
+  launch_cfg<MODE, ST, 128, 128, 2, 2>(p);
+}
+
+template <int MODE>
+void launch_st(const GemmProblem& p) {
   switch (p.st) {
-    case AWQ_F32: launch_typed<MODE, AWQ_F32>(p); break;
-    case AWQ_F16: launch_typed<MODE, AWQ_F16>(p); break;
-    default: launch_typed<MODE, AWQ_BF16>(p); break;
+    case AWQ_F32: launch_mode<MODE, AWQ_F32>(p); break;
+    case AWQ_F16: launch_mode<MODE, AWQ_F16>(p); break;
+    default: launch_mode<MODE, AWQ_BF16>(p); break;
   }
 }
 
@@ -353,12 +781,12 @@ void launch_gemm(const GemmProblem& p) {
   AWQ_ASSERT(p.rows < (1ll << 31) && p.K < (1ll << 31) && p.N < (1ll << 31) &&
                  p.rows * p.K < (1ll << 40) && p.K * (p.N / 8) < (1ll << 31),
              "prefill GEMM: tensor too large");
-  const int64_t tiles = ((p.rows + kBM - 1) / kBM) * ((p.N + kBN - 1) / kBN);
+  const int64_t tiles = ((p.rows + 127) / 128) * ((p.N + 127) / 128);
   AWQ_ASSERT(tiles < (1ll << 31), "prefill GEMM: too many tiles");
   switch (p.xt) {
-    case AWQ_F16: launch_mode<MODE_F16>(p); break;
-    case AWQ_BF16: launch_mode<MODE_BF16>(p); break;
-    default: launch_mode<MODE_F32>(p); break;
+    case AWQ_F16: launch_st<MODE_F16>(p); break;
+    case AWQ_BF16: launch_st<MODE_BF16>(p); break;
+    default: launch_st<MODE_F32>(p); break;
   }
 }
 
