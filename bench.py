@@ -41,8 +41,9 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20000, help="timed decode calls")
     ap.add_argument("--warmup", type=int, default=500, help="untimed decode calls")
-    ap.add_argument("--only", choices=["decode", "prefill", "dequant"], default=None,
-                    help="run one workload only (profiling runs)")
+    ap.add_argument("--only", choices=["decode", "prefill", "dequant", "copy"], default=None,
+                    help="run one workload only (profiling runs); 'copy' is a plain 256 MiB "
+                         "device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     return ap.parse_args()
@@ -79,8 +80,10 @@ def main():
     run_stream = torch.cuda.Stream()  # warm-up, capture, replay and events all on it
 
     def graph_time(launch, per_graph, warmup, steps):
-        """ms per call: `launch(i)` captured `per_graph` times into a graph,
-        replayed until `steps` calls; events on the launch stream."""
+        """ms per call over exactly `steps` calls: `launch(i)` captured into a
+        graph of `per_graph` calls (plus one graph for the remainder), replayed;
+        events on the launch stream, device synchronised on both sides."""
+        per_graph = max(1, min(per_graph, steps))
         torch.cuda.synchronize()
         with torch.cuda.stream(run_stream):
             # Warm-up on the capture stream: the library's per-stream split-K
@@ -88,25 +91,31 @@ def main():
             for i in range(max(warmup, 1)):
                 launch(i)
         torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=run_stream):
-            for i in range(per_graph):
-                launch(i)
-        reps = max(1, math.ceil(steps / per_graph))
+        reps, rem = divmod(steps, per_graph)
+        graphs = []
+        for n_calls, n_reps in ((per_graph, reps), (rem, 1)):
+            if n_calls == 0 or n_reps == 0:
+                continue
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=run_stream):
+                for i in range(n_calls):
+                    launch(i)
+            graphs.append((g, n_reps))
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(run_stream):
-            g.replay()
+            graphs[0][0].replay()  # untimed: first replay uploads the graph
             torch.cuda.synchronize()
             t0 = time.perf_counter()
             e0.record(run_stream)
-            for _ in range(reps):
-                g.replay()
+            for g, n_reps in graphs:
+                for _ in range(n_reps):
+                    g.replay()
             e1.record(run_stream)
             e1.synchronize()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        ms = e0.elapsed_time(e1) / (reps * per_graph)
-        return ms, reps * per_graph, wall
+        ms = e0.elapsed_time(e1) / steps
+        return ms, steps, wall
 
     out = {}
     traffic = {}
@@ -122,6 +131,8 @@ def main():
         qz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, K // G, N // 8).view(np.int32)).to(dev)
         sc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (K // G, N), 0.002, 0.02, np.float16)).to(dev)
         x = torch.from_numpy(synth.normal(synth.TID_X, (M, K), np.float32)).to(dev)
+        # 17 copies: any copy is reused only after >= 15 other calls (459 MB) even
+        # across graph replays of 100 calls, so the 256 MB MALL cannot hold it.
         copies = math.ceil(512e6 / dec_bytes)
         ws = [(qw.clone(), qz.clone(), sc.clone()) for _ in range(copies)]
         y = torch.empty((M, N), dtype=torch.float32, device=dev)
@@ -130,7 +141,7 @@ def main():
             w = ws[i % copies]
             call_gemm(x, _lib.AWQ_F32, w[0], w[1], w[2], _lib.AWQ_F16, y, _lib.AWQ_F32, M, K, N, G)
 
-        ms, calls, wall = graph_time(dec, copies * 6, args.warmup, args.steps)
+        ms, calls, wall = graph_time(dec, 100, args.warmup, args.steps)
         gbs = dec_bytes / (ms * 1e-3) / 1e9
         out["decode"] = dict(ms=ms, calls=calls, wall_s=wall, gbs=gbs, bytes=dec_bytes, copies=copies)
         del ws
@@ -172,6 +183,16 @@ def main():
         ms, calls, wall = graph_time(deq, 20, 10, steps)
         out["dequant"] = dict(ms=ms, calls=calls, wall_s=wall, gbs=dq_bytes / (ms * 1e-3) / 1e9,
                               bytes=dq_bytes)
+
+    # ---------------- counter calibration: plain 256 MiB device copy ----------------------
+    if args.only == "copy":
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(max(1, args.warmup)):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": src.numel() * 4, "calls": max(1, args.warmup)}))
+        return
 
     # ---------------- CPU baseline (oracle, host cores) -----------------------------------
     cpu = None
