@@ -360,6 +360,11 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
 //   per 16-k slice: MFMAs of stage s, then dequantise two columns of W(s+1)
 //   (loaded a stage ago) into the other buffer; one barrier.
 // ===========================================================================
+// s_waitcnt immediate (gfx9 encoding): vmcnt in bits 3:0 and 15:14, expcnt
+// 6:4 (left at its maximum), lgkmcnt 11:8.
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | ((lgkm & 0xF) << 8);
+}
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
 // Packed lane L of two words as f16x2 magic numbers: the byte holding lane L
@@ -392,8 +397,11 @@ struct BigTile {
   static constexpr int kWThreads = kPacks * (kBK / kRW);
   static constexpr int kABytes = BM * kRowBytes;  // one X buffer
   static constexpr int kBBytes = BN * kRowBytes;  // one W buffer
-  // Layout: X buffer 0, X buffer 1, W buffer 0, W buffer 1.
-  static constexpr size_t kSmem = 2 * (size_t)(kABytes + kBBytes);
+  // X is prefetched two stages ahead: three X buffers when they fit in the
+  // 160 KB of LDS next to the two W buffers.
+  static constexpr int kNA = (3 * kABytes + 2 * kBBytes <= 160 * 1024) ? 3 : 2;
+  // Layout: X buffers 0..kNA-1, then W buffers 0, 1.
+  static constexpr size_t kSmem = (size_t)kNA * kABytes + 2 * (size_t)kBBytes;
   static_assert(MODE != MODE_F32, "large-tile kernel is f16/bf16 only");
   static_assert(kWThreads <= kThreads, "W tile needs more threads");
   static_assert((BM / 8) % (kThreads / 64) == 0, "X tile must split evenly over the waves");
@@ -441,9 +449,13 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 
   // ---- W: thread covers pack wp, rows wq*RW .. wq*RW+RW-1 of each stage ----
+  // RW = 8: consecutive lanes take consecutive packs; their 16-byte LDS
+  // writes land in 8 distinct slots. RW = 4: lane bit 0 picks the half
+  // granule (k 0-3 or 4-7) and the next bits the pack, so 16 consecutive
+  // lanes' 8-byte writes cover all 32 banks once.
   const bool w_act = tid < C::kWThreads;
-  const int wp = tid % C::kPacks;
-  const int wq = w_act ? tid / C::kPacks : 0;
+  const int wp = (RW == 8) ? tid % C::kPacks : (tid >> 1) % C::kPacks;
+  const int wq = !w_act ? 0 : (RW == 8) ? tid / C::kPacks : 2 * (tid / (2 * C::kPacks)) + (tid & 1);
   const int pack = min((n0 >> 3) + wp, np - 1);  // ragged N: clamp, never stored
   const rsrc_t wres = make_rsrc(a.qweight, (uint32_t)((int64_t)a.K * np * 4));
   const rsrc_t zres = make_rsrc(a.qzeros, (uint32_t)((int64_t)(a.K / a.group) * np * 4));
@@ -462,12 +474,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     uint32_t z;
     uint32_t sv[kSW];
   };
-  WRegs wa, wb;
+  // W(j) lives in wr[j % 2]: loaded two stages ahead of its MFMAs.
+  WRegs wr[2];
 
   auto load_w = [&](int s, WRegs& r_) {
     const int k0 = s * kBK;
 #pragma unroll
-    for (int r = 0; r < RW; ++r) r_.w[r] = buf_load_u32_nt(wres, wvoff, (uint32_t)(k0 + r) * row_bytes);
+    // Plain (cached) loads: every row tile of the grid re-reads this W block,
+    // from L2 when the tiles sharing it run close together.
+    for (int r = 0; r < RW; ++r) r_.w[r] = buf_load_u32(wres, wvoff, (uint32_t)(k0 + r) * row_bytes);
     const int grp = s >> a.grp_shift;  // a 64-row stage lies in one group
     r_.z = buf_load_u32(zres, (uint32_t)(grp * np + pack) * 4u, 0);
     const uint32_t soff = (uint32_t)(grp * a.N + pack * 8) * (uint32_t)sizeof(S);
@@ -536,7 +551,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     }
     uint32_t off = wl0;
     asm volatile("" : "+v"(off));  // recompute per use: keeps 8 addresses out of the register file
-    unsigned char* dst = smem_raw + ((off ^ (uint32_t)(c << 4)) + (uint32_t)(2 * C::kABytes + buf * C::kBBytes + c * C::kRowBytes));
+    unsigned char* dst = smem_raw + ((off ^ (uint32_t)(c << 4)) + (uint32_t)(C::kNA * C::kABytes + buf * C::kBBytes + c * C::kRowBytes));
     if constexpr (RW == 8)
       *reinterpret_cast<u32x4*>(dst) = u32x4{dq[0], dq[1], dq[2], dq[3]};
     else
@@ -556,7 +571,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   const uint32_t lr = (uint32_t)(lane & 31);
   const uint32_t a_base = (uint32_t)((wm * C::kWTM) * C::kRowBytes) + lr * C::kRowBytes +
                           (uint32_t)((h ^ swz((int)lr)) << 4);
-  const uint32_t b_base = (uint32_t)(2 * C::kABytes) + (uint32_t)((wn * C::kWTN) * C::kRowBytes) +
+  const uint32_t b_base = (uint32_t)(C::kNA * C::kABytes) + (uint32_t)((wn * C::kWTN) * C::kRowBytes) +
                           lr * C::kRowBytes + (uint32_t)((h ^ swz((int)lr)) << 4);
   const uint32_t a_fl = (uint32_t)(((wm * (C::kWTM / 8)) & 4) << 4);
   const uint32_t b_fl = (uint32_t)(((wn * (C::kWTN / 8)) & 4) << 4);
@@ -564,15 +579,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   const uint32_t b_par[2] = {b_base ^ b_fl, b_base ^ b_fl ^ 64u};
   typedef typename std::conditional<MODE == MODE_F16, f16x8, bf16x8>::type V8;
   typedef V8 Frags[C::kI + C::kJ];
-  auto read_frags = [&](int buf, int kq, Frags& f) {
+  auto read_frags = [&](int abuf, int bbuf, int kq, Frags& f) {
 #pragma unroll
     for (int i = 0; i < C::kI; ++i)
       f[i] = *reinterpret_cast<const V8*>(smem_raw + (a_par[i & 1] ^ (uint32_t)(kq << 5)) +
-                                          (buf * C::kABytes + i * 32 * C::kRowBytes));
+                                          (abuf * C::kABytes + i * 32 * C::kRowBytes));
 #pragma unroll
     for (int j = 0; j < C::kJ; ++j)
       f[C::kI + j] = *reinterpret_cast<const V8*>(smem_raw + (b_par[j & 1] ^ (uint32_t)(kq << 5)) +
-                                                  (buf * C::kBBytes + j * 32 * C::kRowBytes));
+                                                  (bbuf * C::kBBytes + j * 32 * C::kRowBytes));
   };
   auto mfmas = [&](const Frags& f) {
 #pragma unroll
@@ -586,24 +601,39 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       }
   };
 
+  // VMEM instructions one stage issues: packed W rows, the zero word, the
+  // scales (16 bytes each), the LDS-direct X granules.
+  constexpr int kVmPerStage = RW + 1 + (kSW + 3) / 4 + kXIns;
+  static_assert(kVmPerStage < 64, "vmcnt range");
+  constexpr int kNA = C::kNA;
+  // End-of-stage wait: with three X buffers the X loads of stage s+1 were
+  // issued a stage earlier, so this stage's loads may stay in flight; with
+  // two they were issued last in this stage and everything must land.
+  constexpr int kVmWait = (kNA == 3) ? kVmPerStage : 0;
+
   // ---- prologue ------------------------------------------------------------
+  load_w(0, wr[0]);
   load_x(0, 0);
-  load_w(0, wa);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
 #pragma unroll
-  for (int c = 0; c < 8; ++c) deq_store_col(wa, c, 0);
-  load_w(min(1, stages - 1), wa);
-  __syncthreads();
+  for (int c = 0; c < 8; ++c) deq_store_col(wr[0], c, 0);
+  load_w(min(1, stages - 1), wr[1]);
+  if constexpr (kNA == 3) load_x(min(1, stages - 1), 1);
+  __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmWait, 0));
+  __builtin_amdgcn_s_barrier();
 
   // ---- main loop -----------------------------------------------------------
-  // Branch-free body: at the tail the prefetches clamp to the last stage and
-  // the writes go to the buffer nobody reads any more, so one basic block
-  // holds the loads, the dequantisation and the MFMAs for the scheduler to
-  // interleave. The barrier also waits for the LDS-direct loads (vmcnt), so
-  // W for stage s+2 lands by the end of stage s and is dequantised in s+1.
-  // Unrolled by two so the register sets alternate without copies.
-  // Instruction order inside one 16-k slice: the operand reads for the next
-  // slice first, then each MFMA followed by a few dequantisation VALU ops
-  // (they run while the matrix core is busy), then the LDS writes.
+  // Stage s reads X buffer s % kNA and W buffer s % 2. It issues the packed
+  // W / zeros / scales of stage s+2 (registers) and then the LDS-direct X
+  // loads of stage s+2 (buffer (s+2) % kNA; with kNA == 2 X goes one stage
+  // ahead instead), dequantises W(s+1) into W buffer (s+1) % 2 while its
+  // MFMAs run, and ends with an explicit wait: vmcnt(loads issued in this
+  // stage) leaves this stage's prefetches in flight but guarantees the X of
+  // stage s+1 has landed, lgkmcnt(0) completes this wave's LDS writes; then
+  // the barrier. (A plain s_barrier, not __syncthreads(): the latter would
+  // also wait for the X loads just issued.) The body is branch-free: at the
+  // tail the prefetches clamp to the last stage and land in buffers nobody
+  // reads any more.
   auto interleave = [&]() {
     constexpr int kM = C::kI * C::kJ;
     __builtin_amdgcn_sched_group_barrier(0x100, C::kI + C::kJ, 0);  // DS read
@@ -614,35 +644,41 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     }
     __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);  // DS write
   };
-  // Within a stage the operand reads for slice kq+1 are issued before the
-  // MFMAs of slice kq; scheduling fences keep each slice's reads, MFMAs and
-  // dequantisation together so the live registers stay bounded.
-  auto step = [&](int s, int buf, WRegs& deq, WRegs& next) {
-    load_x(min(s + 1, stages - 1), buf ^ 1);
-    load_w(min(s + 2, stages - 1), next);
+  constexpr int kXAhead = (kNA == 3) ? 2 : 1;
+  auto step = [&](int s, int abuf, int bbuf, WRegs& deq, WRegs& next) {
     Frags f0, f1;
-    read_frags(buf, 0, f0);
+    read_frags(abuf, bbuf, 0, f0);
+    load_w(min(s + 2, stages - 1), next);
+    __builtin_amdgcn_sched_barrier(0);
+    load_x(min(s + kXAhead, stages - 1), (abuf + kXAhead) % kNA);
 #pragma unroll
     for (int kq = 0; kq < kBK / 16; kq += 2) {
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(buf, kq + 1, f1);
+      read_frags(abuf, bbuf, kq + 1, f1);
       mfmas(f0);
-      deq_store_col(deq, 2 * kq, buf ^ 1);
-      deq_store_col(deq, 2 * kq + 1, buf ^ 1);
+      deq_store_col(deq, 2 * kq, bbuf ^ 1);
+      deq_store_col(deq, 2 * kq + 1, bbuf ^ 1);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
-      if (kq + 2 < kBK / 16) read_frags(buf, kq + 2, f0);
+      if (kq + 2 < kBK / 16) read_frags(abuf, bbuf, kq + 2, f0);
       mfmas(f1);
-      deq_store_col(deq, 2 * kq + 2, buf ^ 1);
-      deq_store_col(deq, 2 * kq + 3, buf ^ 1);
+      deq_store_col(deq, 2 * kq + 2, bbuf ^ 1);
+      deq_store_col(deq, 2 * kq + 3, bbuf ^ 1);
       interleave();
     }
     __builtin_amdgcn_sched_barrier(0);
-    __syncthreads();
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmWait, 0));
+    __builtin_amdgcn_s_barrier();
   };
-  for (int s = 0; s < stages; s += 2) {
-    step(s, 0, wa, wb);
-    if (s + 1 < stages) step(s + 1, 1, wb, wa);
+  // Unrolled over lcm(kNA, 2) stages so buffers and register sets are
+  // compile-time: step s dequantises W(s+1) from wr[(s+1) % 2] and loads
+  // W(s+2) into wr[s % 2], whose W(s) was dequantised in step s-1.
+  constexpr int kU = (kNA == 3) ? 6 : 2;
+  for (int s = 0; s < stages; s += kU) {
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      if (u == 0 || s + u < stages) step(s + u, u % kNA, u % 2, wr[(u + 1) % 2], wr[u % 2]);
+    }
   }
 
   // ---- epilogue --------------------------------------------------------------
@@ -760,6 +796,7 @@ void launch_mode(const GemmProblem& p) {
       case 3: return launch_big<MODE, ST, 128, 256, 2, 4>(p);
       case 4: return launch_big<MODE, ST, 128, 128, 2, 2>(p);
       case 6: return launch_big<MODE, ST, 256, 128, 4, 2>(p);
+      case 7: return launch_big<MODE, ST, 256, 256, 2, 2>(p);
       default: break;
     }
   }
