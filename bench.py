@@ -53,8 +53,8 @@ def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(the per-GPU shard is the single-GPU kernel; see DESIGN.md).", file=sys.stderr)
+        print("bench.py measures one GPU: there is no multi-GPU path here; a sharded "
+              "deployment runs this single-GPU kernel on each GPU's shard.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

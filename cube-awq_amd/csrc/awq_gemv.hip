@@ -383,40 +383,53 @@ void launch_cfg(const GemmProblem& p) {
   check_hip(hipGetLastError(), "gemv kernel launch");
 }
 
-// Rows per wave (a multiple of 4 dividing the group size, <= 128) and waves per
-// workgroup: enough workgroups to occupy the CUs (>= 192) with as few K splits
-// as possible, since each split adds a partial round trip at the end.
+// Largest rows-per-wave a (x dtype, rows, waves) instantiation holds in
+// registers without spilling: two batches of up to 32 weight words per lane
+// plus the row accumulators, within 512 / waves-per-SIMD VGPRs (f16/bf16
+// activations need a few more for the conversions).
+constexpr int rpw_max(int xt, int mt, int waves) {
+  const bool f32 = xt == AWQ_F32;
+  return mt == 1 ? (waves >= 16 ? (f32 ? 96 : 64) : 128)
+       : mt == 2 ? (waves >= 16 ? 8 : waves == 8 ? (f32 ? 16 : 8) : 32)
+       : mt == 4 ? (waves >= 8 ? 16 : 32)
+       : (waves >= 8 ? (f32 ? 16 : 8) : (f32 ? 32 : 16));
+}
+
+// Rows per wave (dividing the group size) and waves per workgroup: enough
+// workgroups to occupy the CUs (>= 192) with as few K splits as possible,
+// since each split adds a partial round trip at the end; never a
+// configuration that spills.
 template <int XT, int MT, int WMAX>
 void launch_rpw(const GemmProblem& p) {
   const int g = (int)p.group;
   const int chunks = (int)((p.N / 8 + 63) / 64);
   int rpw = g % 32 == 0 ? 32 : g % 16 == 0 ? 16 : g % 8 == 0 ? 8 : 4;
-  if (MT >= 4 && rpw > 16) rpw = 16;  // register budget of the many-row variants
   int waves = WMAX;
   auto wgs = [&](int w, int r) {
     return (int64_t)chunks * ((p.K + (int64_t)w * r - 1) / ((int64_t)w * r));
   };
-  while (waves > 4 && wgs(waves, rpw) < 192) waves >>= 1;
+  auto cap = [&](int w, int r) {
+    while (r > rpw_max(XT, MT, w)) r >>= 1;
+    return r;
+  };
+  while (waves > 4 && wgs(waves, cap(waves, rpw)) < 192) waves >>= 1;
+  rpw = cap(waves, rpw);
   // Long runs per wave (fewer splits) while the workgroup count stays high.
-  while (MT <= 2 && rpw < 128 && g % (2 * rpw) == 0 && wgs(waves, 2 * rpw) >= 192) rpw *= 2;
-  if (int v = env_int("AWQ_GEMV_WAVES", 0); v == 4 || v == 8 || v == 16) waves = v > WMAX ? WMAX : v;
-  if (int v = env_int("AWQ_GEMV_RPW", 0); v >= 4 && v <= 128 && g % v == 0 &&
-                                          (v == 4 || v == 8 || v == 16 || v % 32 == 0))
-    rpw = v;
+  while (rpw < 128 && 2 * rpw <= rpw_max(XT, MT, waves) && g % (2 * rpw) == 0 &&
+         wgs(waves, 2 * rpw) >= 192)
+    rpw *= 2;
+  if (int v = env_int("AWQ_GEMV_WAVES", 0); (v == 4 || v == 8 || v == 16) && v <= WMAX) waves = v;
+  if (int v = env_int("AWQ_GEMV_RPW", 0); v >= 4 && g % v == 0) rpw = v;
+  rpw = cap(waves, rpw);
+  while (g % rpw != 0) rpw >>= 1;
 #define AWQ_GEMV_CASE(W, R) \
-  if (waves == W && rpw == R) return launch_cfg<XT, MT, W, R>(p);
-#define AWQ_GEMV_WCASES(W) \
-  AWQ_GEMV_CASE(W, 4) AWQ_GEMV_CASE(W, 8) AWQ_GEMV_CASE(W, 16) AWQ_GEMV_CASE(W, 32)
-  if constexpr (WMAX >= 16) {
-    AWQ_GEMV_WCASES(16)
-    if constexpr (MT <= 2) { AWQ_GEMV_CASE(16, 64) AWQ_GEMV_CASE(16, 96) AWQ_GEMV_CASE(16, 128) }
-  }
+  if constexpr (R <= rpw_max(XT, MT, W)) { if (waves == W && rpw == R) return launch_cfg<XT, MT, W, R>(p); }
+#define AWQ_GEMV_WCASES(W)                                                                    \
+  AWQ_GEMV_CASE(W, 4) AWQ_GEMV_CASE(W, 8) AWQ_GEMV_CASE(W, 16) AWQ_GEMV_CASE(W, 32)          \
+  AWQ_GEMV_CASE(W, 64) AWQ_GEMV_CASE(W, 96) AWQ_GEMV_CASE(W, 128)
+  if constexpr (WMAX >= 16) { AWQ_GEMV_WCASES(16) }
   AWQ_GEMV_WCASES(8)
   AWQ_GEMV_WCASES(4)
-  if constexpr (MT <= 2) {
-    AWQ_GEMV_CASE(8, 64) AWQ_GEMV_CASE(8, 96) AWQ_GEMV_CASE(8, 128)
-    AWQ_GEMV_CASE(4, 64) AWQ_GEMV_CASE(4, 96) AWQ_GEMV_CASE(4, 128)
-  }
 #undef AWQ_GEMV_WCASES
 #undef AWQ_GEMV_CASE
   panic("decode GEMV: no kernel configuration for this shape");
