@@ -108,6 +108,9 @@ __device__ __forceinline__ uint32_t buf_load_u32(rsrc_t r, uint32_t voff, uint32
 // Same with the nontemporal (nt) cache policy: for data read exactly once
 // (the weight stream), so it does not displace reused lines in L2.
 constexpr int kCachePolicyNT = 2;
+// Device-coherent (agent scope) access: sc1, as agent-scope atomic loads and
+// stores use, so data written by other workgroups' sc1 stores is seen.
+constexpr int kCachePolicySC1 = 16;
 __device__ __forceinline__ uint32_t buf_load_u32_nt(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kCachePolicyNT);
 }

@@ -29,6 +29,7 @@
 // v_pk_mul_f16 applies the scale: the result is the correctly rounded f16 of
 // (q - z) * s, the value the reference computes with F = f16. Odd packed
 // lanes (high nibble of the byte) take one extra shift.
+#include <algorithm>
 #include <cstdlib>
 #include <type_traits>
 
@@ -74,7 +75,15 @@ struct GemmArgs {
   int32_t tiles_m, tiles_n;
   int32_t swizzled_tiles;  // leading tiles covered by the XCD mapping (multiple of 8)
   int32_t grp_shift;       // large-tile kernel: group = 64 << grp_shift
+  // Large-tile kernel split-K (grid.y = splits): workgroup y covers stages
+  // [y * stages_per_split, ...); partials [splits][M][N] and one arrival
+  // counter per tile (kTileCtrStride apart, zero between calls).
+  int32_t splits, stages_per_split;
+  float* partial;
+  uint32_t* counters;
 };
+
+constexpr int kTileCtrStride = 64;  // u32 words between per-tile counters (256 B)
 
 __device__ __forceinline__ uint32_t perm_b32(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
@@ -430,7 +439,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   const int tile_n = t / a.tiles_m;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int np = a.N >> 3;
-  const int stages = a.K / kBK;
+  // K range of this workgroup: all of K, or its split's run of stages.
+  const int split = blockIdx.y;
+  const int s_begin = split * a.stages_per_split;
+  const int stages = min(a.stages_per_split, a.K / kBK - s_begin);
 
   // ---- X: copied global -> LDS directly (buffer_load ... lds). One
   // instruction moves 64 x 16 bytes into 1 KB of LDS, lane l landing in row
@@ -478,6 +490,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   WRegs wr[2];
 
   auto load_w = [&](int s, WRegs& r_) {
+    s += s_begin;
     const int k0 = s * kBK;
 #pragma unroll
     // Plain (cached) loads: every row tile of the grid re-reads this W block,
@@ -501,7 +514,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   };
 
   auto load_x = [&](int s, int buf) {
-    const uint32_t koff = (uint32_t)(s * kBK) * 2u;
+    const uint32_t koff = (uint32_t)((s_begin + s) * kBK) * 2u;
 #pragma unroll
     for (int i = 0; i < kXIns; ++i) {
       lds_dma16(xres, smem_raw + buf * C::kABytes + (wave + i * NW) * 1024, xvoff[i], koff);
@@ -682,6 +695,76 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 
   // ---- epilogue --------------------------------------------------------------
+  if (a.splits > 1) {
+    // Split-K: publish this split's tile with agent-scope (write-through)
+    // stores, wait for them, count the arrival; the last workgroup of the tile
+    // re-reads all splits' partials (agent-scope loads, split order, in a
+    // coalesced row-major walk of the tile), adds the bias and writes y, and
+    // re-arms the counter.
+    float* part = a.partial + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int j = 0; j < C::kJ; ++j) {
+      const int n = n0 + wn * C::kWTN + 32 * j + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (m < a.M && n < a.N)
+            __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][j][r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // The flag lives in the (now idle) tile buffers: a static __shared__
+    // variable would push the 160 KB configuration over the LDS limit.
+    volatile int* s_last = reinterpret_cast<volatile int*>(smem_raw);
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[t * kTileCtrStride], 1u,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    // 4 consecutive columns per thread and step (N % 8 == 0 keeps a group of
+    // 4 inside the row), agent-scope (sc1) loads, 8 splits in flight.
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
+    const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
+    for (int e = tid * 4; e < BM * BN; e += C::kThreads * 4) {
+      const int m = m0 + e / BN, n = n0 + e % BN;
+      if (m >= a.M || n >= a.N) continue;
+      const uint32_t off = (uint32_t)(((int64_t)m * a.N + n) * 4);
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < a.splits; s0 += 8) {
+        // Every slot is loaded (split index clamped) and only the valid ones
+        // are added, so nothing read is ever undefined.
+        uint32_t t8[8][4];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            t8[j][q] = __builtin_amdgcn_raw_buffer_load_b32(
+                pres, off + 4u * q, (uint32_t)min(s0 + j, a.splits - 1) * sstride, kCachePolicySC1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const bool ok = s0 + j < a.splits;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[q] += ok ? __builtin_bit_cast(float, t8[j][q]) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float o = v[q];
+        if (a.bias) o += load_f32_any(a.bias, n + q, a.bt);
+        store_f32_any(a.y, (int64_t)m * a.N + n + q, a.yt, o);
+      }
+    }
+    if (tid == 0)
+      __hip_atomic_store(&a.counters[t * kTileCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < C::kJ; ++j) {
     const int n = n0 + wn * C::kWTN + 32 * j + (lane & 31);
@@ -699,7 +782,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 }
 
 template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
-void launch_big(const GemmProblem& p) {
+void launch_big(const GemmProblem& p, int splits = 1) {
   using C = BigTile<MODE, BM, BN, WGM, WGN>;
   GemmArgs a{};
   a.x = p.x;
@@ -720,6 +803,17 @@ void launch_big(const GemmProblem& p) {
   const int tiles = a.tiles_m * a.tiles_n;
   a.swizzled_tiles = tiles & ~7;
   a.grp_shift = __builtin_ctzll(p.group / kBK);
+  const int total_stages = (int)(p.K / kBK);
+  // Partials are addressed through a 32-bit buffer range.
+  while (splits > 1 && (int64_t)splits * p.rows * p.N * 4 >= (1ll << 32)) --splits;
+  a.stages_per_split = (total_stages + splits - 1) / splits;
+  a.splits = (total_stages + a.stages_per_split - 1) / a.stages_per_split;  // no empty split
+  if (a.splits > 1) {
+    a.counters = static_cast<uint32_t*>(
+        workspace_get(p.stream, (size_t)tiles * kTileCtrStride * sizeof(uint32_t), kWsCounters));
+    a.partial = static_cast<float*>(
+        workspace_get(p.stream, (size_t)a.splits * p.rows * p.N * sizeof(float), kWsPartials));
+  }
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
     check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>,
@@ -727,8 +821,8 @@ void launch_big(const GemmProblem& p) {
               "hipFuncSetAttribute(gemm_big)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>), dim3(tiles), dim3(C::kThreads),
-                     C::kSmem, p.stream, a);
+  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>), dim3(tiles, a.splits),
+                     dim3(C::kThreads), C::kSmem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
 
@@ -753,6 +847,7 @@ void launch_cfg(const GemmProblem& p) {
   a.tiles_n = (int)((p.N + BN - 1) / BN);
   const int tiles = a.tiles_m * a.tiles_n;
   a.swizzled_tiles = tiles & ~7;
+  a.splits = 1;
   const size_t smem = C::kSmem;
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
@@ -783,20 +878,32 @@ void launch_mode(const GemmProblem& p) {
                       p.rows * p.K * 2 < (1ll << 32) && p.K * (p.N / 8) * 4 < (1ll << 32) &&
                       (p.K / p.group) * p.N * 4 < (1ll << 32);
   if (!big_ok) cfg = 1;
+  auto tiles = [&](int bm, int bn) { return ((p.rows + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
+  int splits = 1;
   if (cfg == 0) {
-    auto tiles = [&](int bm, int bn) { return ((p.rows + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
     if (tiles(256, 256) >= 240) cfg = 2;
-    else if (tiles(128, 256) >= 240) cfg = 3;
-    else if (tiles(128, 128) >= 120) cfg = 4;
-    else cfg = 1;
+    else if (tiles(128, 256) >= 200) cfg = 3;
+    else {
+      cfg = 4;  // 128 x 128 tiles, two workgroups per CU
+      if (p.rows <= 128) {
+        // Skinny problems: split K across workgroups until ~320 are in
+        // flight (at most 8 splits, at least 4 stages each). Larger M keeps
+        // one split: its partials would cost more HBM traffic than they save.
+        const int64_t t = tiles(128, 128);
+        const int64_t stages = p.K / kBK;
+        splits = (int)std::min<int64_t>({(320 + t - 1) / t, 8, std::max<int64_t>(stages / 4, 1)});
+      }
+    }
   }
+  if (int v = env_int("AWQ_GEMM_SPLITS", 0); v >= 1) splits = v;
   if constexpr (MODE != MODE_F32) {
     switch (cfg) {
-      case 2: return launch_big<MODE, ST, 256, 256, 2, 4>(p);
-      case 3: return launch_big<MODE, ST, 128, 256, 2, 4>(p);
-      case 4: return launch_big<MODE, ST, 128, 128, 2, 2>(p);
-      case 6: return launch_big<MODE, ST, 256, 128, 4, 2>(p);
-      case 7: return launch_big<MODE, ST, 256, 256, 2, 2>(p);
+      case 2: return launch_big<MODE, ST, 256, 256, 2, 4>(p, splits);
+      case 3: return launch_big<MODE, ST, 128, 256, 2, 4>(p, splits);
+      case 4: return launch_big<MODE, ST, 128, 128, 2, 2>(p, splits);
+      case 6: return launch_big<MODE, ST, 256, 128, 4, 2>(p, splits);
+      case 7: return launch_big<MODE, ST, 256, 256, 2, 2>(p, splits);
+      case 8: return launch_big<MODE, ST, 64, 256, 1, 8>(p, splits);
       default: break;
     }
   }
