@@ -8,4 +8,4 @@ from .kernel import (  # noqa: F401
     DECODE_M_THRESHOLD, DECODE_TILE_M, ShapeConfig, awq_gemm_linear, dequantize_awq,
     dequantize_native, validate_decode_launch_params, validate_launch_params)
 from .modules import AWQGEMMLinear, AWQGEMMLinearConfig, AWQLinear, AWQLinearConfig  # noqa: F401
-from . import pack  # noqa: F401
+from . import checkpoint, pack  # noqa: F401

@@ -1,0 +1,69 @@
+"""AutoAWQ checkpoint ingestion (safetensors naming, int32 words kept bit for
+bit, the module constraints and messages), CPU only; the GPU test runs the
+loaded layer against the oracle."""
+import numpy as np
+import pytest
+import torch
+
+from cube_awq import checkpoint, synth
+from cube_awq._lib import Panic
+from cube_awq.modules import AWQGEMMLinear, AWQLinear
+
+
+def _tensors(k=256, n=128, g=64, bias=True):
+    qw = torch.from_numpy(synth.packed_nibbles(synth.TID_QWEIGHT, k, n // 8).view(np.int32).copy())
+    qz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, k // g, n // 8).view(np.int32).copy())
+    sc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (k // g, n), 0.002, 0.02, np.float16))
+    d = {"model.layers.0.mlp.up_proj.qweight": qw, "model.layers.0.mlp.up_proj.qzeros": qz,
+         "model.layers.0.mlp.up_proj.scales": sc}
+    if bias:
+        d["model.layers.0.mlp.up_proj.bias"] = torch.from_numpy(
+            synth.uniform(synth.TID_BIAS, (n,), -1.0, 1.0, np.float16))
+    return d
+
+
+def test_roundtrip_through_safetensors(tmp_path):
+    d = _tensors()
+    layer = checkpoint.load_awq_gemm_linear(d, "model.layers.0.mlp.up_proj")
+    assert isinstance(layer, AWQGEMMLinear) and layer.group_size() == 64
+    path = str(tmp_path / "layer.safetensors")
+    checkpoint.save({"model.layers.0.mlp.up_proj": layer}, path)
+    again = checkpoint.load_awq_gemm_linear(path, "model.layers.0.mlp.up_proj")
+    for name in ("qweight", "qzeros", "scales", "bias"):
+        a, b = getattr(layer, name), getattr(again, name)
+        assert a.dtype == b.dtype and torch.equal(a, b), name
+    # int32 words with the top bit set survive unchanged (read as uint32 by the kernels)
+    assert (again.qweight < 0).any()
+
+
+def test_optional_bias_and_scale_cast():
+    d = _tensors(bias=False)
+    layer = checkpoint.load_awq_gemm_linear(d, "model.layers.0.mlp.up_proj", scale_dtype=torch.float32)
+    assert layer.bias is None and layer.scales.dtype == torch.float32
+    lin = checkpoint.load_awq_linear(d, "model.layers.0.mlp.up_proj")
+    assert isinstance(lin, AWQLinear) and lin.group_size() == 64
+
+
+@pytest.mark.parametrize("mutate, msg", [
+    (lambda d: d.pop("model.layers.0.mlp.up_proj.qzeros"), "no tensor"),
+    (lambda d: d.__setitem__("model.layers.0.mlp.up_proj.qweight",
+                             d["model.layers.0.mlp.up_proj.qweight"].to(torch.int64)), "32-bit elements"),
+    (lambda d: d.__setitem__("model.layers.0.mlp.up_proj.scales",
+                             d["model.layers.0.mlp.up_proj.scales"][:, :64]), "columns"),
+    (lambda d: d.__setitem__("model.layers.0.mlp.up_proj.qzeros",
+                             d["model.layers.0.mlp.up_proj.qzeros"][:2]), "qzeros must be"),
+])
+def test_rejections(mutate, msg):
+    d = _tensors()
+    mutate(d)
+    with pytest.raises(Panic, match=msg):
+        checkpoint.load_awq_gemm_linear(d, "model.layers.0.mlp.up_proj")
+
+
+def test_gemm_constraints_apply():
+    # K = 96 is a multiple of the group (32) but not of INNER_K (64)
+    qw = torch.zeros((96, 4), dtype=torch.int32)
+    qz = torch.zeros((3, 4), dtype=torch.int32)
+    sc = torch.ones((3, 32), dtype=torch.float16)
+    with pytest.raises(Panic, match="INNER_K"):
+        checkpoint.load_awq_gemm_linear({"l.qweight": qw, "l.qzeros": qz, "l.scales": sc}, "l")

@@ -70,3 +70,26 @@ def test_forward_on_non_default_stream(dev):
         y = lay.forward(xd)
     s.synchronize()
     assert oracle.rel_l2(y.cpu().numpy(), oracle.gemm_f64(x.numpy(), qw, qz, sc, g)) <= 1e-5
+
+
+@pytest.mark.parametrize("M", [1, 300])
+def test_checkpoint_loaded_layer_forward(dev, tmp_path, M):
+    """An AutoAWQ-named safetensors file (int32 words, f16 scales, bias) loads
+    into AWQGEMMLinear and runs on both paths (decode M = 1, prefill M = 300)."""
+    from cube_awq import checkpoint
+    K, N, g = 512, 256, 128
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt="f16", bias=True)
+    path = str(tmp_path / "awq.safetensors")
+    from safetensors.torch import save_file
+    save_file({"blk.qweight": torch.from_numpy(pack.as_int32(qw)),
+               "blk.qzeros": torch.from_numpy(pack.as_int32(qz)),
+               "blk.scales": torch.from_numpy(sc.astype(np.float16)),
+               "blk.bias": torch.from_numpy(b.astype(np.float16))}, path)
+    lay = checkpoint.load_awq_gemm_linear(path, "blk", device=dev)
+    xt = torch.from_numpy(x.astype(np.float16)).to(dev)
+    y = lay.forward(xt)
+    torch.cuda.synchronize()
+    ref = oracle.gemm_f64(x.astype(np.float16).astype(np.float32), qw, qz,
+                          sc.astype(np.float16).astype(np.float32), g,
+                          bias=b.astype(np.float16).astype(np.float32))
+    assert oracle.rel_l2(y.float().cpu().numpy(), ref) <= 2e-3
