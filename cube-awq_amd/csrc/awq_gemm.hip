@@ -394,13 +394,17 @@ __device__ __forceinline__ void lds_dma16(rsrc_t r, unsigned char* dst, uint32_t
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
 }
 
-template <int MODE, int BM, int BN, int WGM, int WGN>
+template <int MODE, int BM, int BN, int WGM, int WGN, int MS>
 struct BigTile {
   typedef typename ModeT<MODE>::T T;
   static constexpr int kThreads = 64 * WGM * WGN;
   static constexpr int kRowBytes = kBK * 2;
   static constexpr int kWTM = BM / WGM, kWTN = BN / WGN;
-  static constexpr int kI = kWTM / 32, kJ = kWTN / 32;
+  // MFMA shape: MS = 32 -> 32x32x16 (16 k per slice), MS = 16 -> 16x16x32.
+  static constexpr int kI = kWTM / MS, kJ = kWTN / MS;
+  static constexpr int kSliceK = MS == 32 ? 16 : 32;
+  static constexpr int kSlices = kBK / kSliceK;
+  static constexpr int kColsPerSlice = 8 / kSlices;  // W columns dequantised per slice
   static constexpr int kPacks = BN / 8;                         // packed words per W row
   static constexpr int kRW = (64 * kPacks / kThreads >= 8) ? 8 : 4;  // W rows per thread
   static constexpr int kWThreads = kPacks * (kBK / kRW);
@@ -414,12 +418,13 @@ struct BigTile {
   static_assert(MODE != MODE_F32, "large-tile kernel is f16/bf16 only");
   static_assert(kWThreads <= kThreads, "W tile needs more threads");
   static_assert((BM / 8) % (kThreads / 64) == 0, "X tile must split evenly over the waves");
-  static_assert(kWTM % 32 == 0 && kWTN % 32 == 0, "wave tile must be whole 32x32 blocks");
+  static_assert(MS == 32 || MS == 16, "MFMA shape");
+  static_assert(kWTM % MS == 0 && kWTN % MS == 0, "wave tile must be whole MFMA blocks");
 };
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a) {
-  using C = BigTile<MODE, BM, BN, WGM, WGN>;
+  using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   using S = typename Elem<ST>::type;
   constexpr int RW = C::kRW;
   constexpr int kSW = (sizeof(S) * 8) / 4;  // dwords holding a pack's 8 scales
@@ -572,11 +577,29 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   };
 
   // ---- MFMA operand addressing -------------------------------------------
-  f32x16 acc[C::kI][C::kJ];
+  typedef float AccT __attribute__((ext_vector_type(MS == 32 ? 16 : 4)));
+  AccT acc[C::kI][C::kJ];
 #pragma unroll
   for (int i = 0; i < C::kI; ++i)
 #pragma unroll
-    for (int j = 0; j < C::kJ; ++j) acc[i][j] = f32x16{};
+    for (int j = 0; j < C::kJ; ++j) acc[i][j] = AccT{};
+  // 16x16x32: lane l reads row (l & 15) of a block, granule 4 kq + (l >> 4);
+  // the slice kq flips granule bit 2 (kq << 6 in bytes), so one base per
+  // block row plus an XOR.
+  uint32_t a16[C::kI], b16[C::kJ];
+  if constexpr (MS == 16) {
+    const int l16 = lane & 15, h4 = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < C::kI; ++i) {
+      const int row = wm * C::kWTM + 16 * i + l16;
+      a16[i] = (uint32_t)(row * C::kRowBytes + ((h4 ^ swz(row)) << 4));
+    }
+#pragma unroll
+    for (int j = 0; j < C::kJ; ++j) {
+      const int col = wn * C::kWTN + 16 * j + l16;
+      b16[j] = (uint32_t)(C::kNA * C::kABytes + col * C::kRowBytes + ((h4 ^ swz(col)) << 4));
+    }
+  }
   const int h = lane >> 5;  // which 8-k half of the 16-k MFMA slice
   // Row wm*WTM + 32 i + (lane & 31): its swizzle is swz(lane & 31) with bit 2
   // flipped by (4 i + wm*WTM/8) & 4, so two base registers per operand and
@@ -593,6 +616,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   typedef typename std::conditional<MODE == MODE_F16, f16x8, bf16x8>::type V8;
   typedef V8 Frags[C::kI + C::kJ];
   auto read_frags = [&](int abuf, int bbuf, int kq, Frags& f) {
+    if constexpr (MS == 16) {
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i)
+        f[i] = *reinterpret_cast<const V8*>(smem_raw + (a16[i] ^ (uint32_t)(kq << 6)) + abuf * C::kABytes);
+#pragma unroll
+      for (int j = 0; j < C::kJ; ++j)
+        f[C::kI + j] = *reinterpret_cast<const V8*>(smem_raw + (b16[j] ^ (uint32_t)(kq << 6)) + bbuf * C::kBBytes);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < C::kI; ++i)
       f[i] = *reinterpret_cast<const V8*>(smem_raw + (a_par[i & 1] ^ (uint32_t)(kq << 5)) +
@@ -607,11 +639,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     for (int i = 0; i < C::kI; ++i)
 #pragma unroll
       for (int j = 0; j < C::kJ; ++j) {
-        if constexpr (MODE == MODE_F16)
+        if constexpr (MS == 16 && MODE == MODE_F16)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(f[i], f[C::kI + j], acc[i][j], 0, 0, 0);
+        else if constexpr (MS == 16)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f[i], f[C::kI + j], acc[i][j], 0, 0, 0);
+        else if constexpr (MODE == MODE_F16)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], f[C::kI + j], acc[i][j], 0, 0, 0);
         else
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[i], f[C::kI + j], acc[i][j], 0, 0, 0);
       }
+  };
+  // Output element r of block (i, j) for this lane: 32x32 blocks hold rows
+  // 8 (r / 4) + 4 (lane / 32) + r % 4 of column lane % 32; 16x16 blocks rows
+  // 4 (lane / 16) + r of column lane % 16.
+  constexpr int kAccN = MS == 32 ? 16 : 4;
+  auto out_row = [&](int i, int r) -> int {
+    if constexpr (MS == 32) return m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    else return m0 + wm * C::kWTM + 16 * i + 4 * (lane >> 4) + r;
+  };
+  auto out_col = [&](int j) -> int {
+    if constexpr (MS == 32) return n0 + wn * C::kWTN + 32 * j + (lane & 31);
+    else return n0 + wn * C::kWTN + 16 * j + (lane & 15);
   };
 
   // VMEM instructions one stage issues: packed W rows, the zero word, the
@@ -649,13 +697,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // reads any more.
   auto interleave = [&]() {
     constexpr int kM = C::kI * C::kJ;
+    constexpr int kValu = MS == 32 ? 4 : 3;  // VALU ops after each MFMA
     __builtin_amdgcn_sched_group_barrier(0x100, C::kI + C::kJ, 0);  // DS read
 #pragma unroll
     for (int q = 0; q < kM; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x002, kValu, 0);  // VALU
     }
-    __builtin_amdgcn_sched_group_barrier(0x200, 4, 0);  // DS write
+    __builtin_amdgcn_sched_group_barrier(0x200, 2 * C::kColsPerSlice, 0);  // DS write
   };
   constexpr int kXAhead = (kNA == 3) ? 2 : 1;
   auto step = [&](int s, int abuf, int bbuf, WRegs& deq, WRegs& next) {
@@ -664,19 +713,20 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     load_w(min(s + 2, stages - 1), next);
     __builtin_amdgcn_sched_barrier(0);
     load_x(min(s + kXAhead, stages - 1), (abuf + kXAhead) % kNA);
+    constexpr int kCPS = C::kColsPerSlice;
 #pragma unroll
-    for (int kq = 0; kq < kBK / 16; kq += 2) {
+    for (int kq = 0; kq < C::kSlices; kq += 2) {
       __builtin_amdgcn_sched_barrier(0);
       read_frags(abuf, bbuf, kq + 1, f1);
       mfmas(f0);
-      deq_store_col(deq, 2 * kq, bbuf ^ 1);
-      deq_store_col(deq, 2 * kq + 1, bbuf ^ 1);
+#pragma unroll
+      for (int c = 0; c < kCPS; ++c) deq_store_col(deq, kq * kCPS + c, bbuf ^ 1);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
-      if (kq + 2 < kBK / 16) read_frags(abuf, bbuf, kq + 2, f0);
+      if (kq + 2 < C::kSlices) read_frags(abuf, bbuf, kq + 2, f0);
       mfmas(f1);
-      deq_store_col(deq, 2 * kq + 2, bbuf ^ 1);
-      deq_store_col(deq, 2 * kq + 3, bbuf ^ 1);
+#pragma unroll
+      for (int c = 0; c < kCPS; ++c) deq_store_col(deq, (kq + 1) * kCPS + c, bbuf ^ 1);
       interleave();
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -704,12 +754,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     float* part = a.partial + (int64_t)split * a.M * a.N;
 #pragma unroll
     for (int j = 0; j < C::kJ; ++j) {
-      const int n = n0 + wn * C::kWTN + 32 * j + (lane & 31);
+      const int n = out_col(j);
 #pragma unroll
       for (int i = 0; i < C::kI; ++i) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        for (int r = 0; r < kAccN; ++r) {
+          const int m = out_row(i, r);
           if (m < a.M && n < a.N)
             __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][j][r], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
@@ -767,23 +817,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 #pragma unroll
   for (int j = 0; j < C::kJ; ++j) {
-    const int n = n0 + wn * C::kWTN + 32 * j + (lane & 31);
+    const int n = out_col(j);
     if (n >= a.N) continue;
     const float bias = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
 #pragma unroll
     for (int i = 0; i < C::kI; ++i) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      for (int r = 0; r < kAccN; ++r) {
+        const int m = out_row(i, r);
         if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][j][r] + bias);
       }
     }
   }
 }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS = 32>
 void launch_big(const GemmProblem& p, int splits = 1) {
-  using C = BigTile<MODE, BM, BN, WGM, WGN>;
+  using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   GemmArgs a{};
   a.x = p.x;
   a.qweight = p.qweight;
@@ -816,12 +866,12 @@ void launch_big(const GemmProblem& p, int splits = 1) {
   }
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kSmem),
               "hipFuncSetAttribute(gemm_big)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN>), dim3(tiles, a.splits),
+  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS>), dim3(tiles, a.splits),
                      dim3(C::kThreads), C::kSmem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
@@ -866,6 +916,20 @@ int env_int(const char* name, int dflt) {
   return e ? std::atoi(e) : dflt;
 }
 
+// Compute units of the current device (queried once per device).
+int64_t num_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int v = 0;
+    check_hip(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    cached[dev] = v > 0 ? v : 256;
+  }
+  return cached[dev];
+}
+
 // Tile choice. f16/bf16 problems with K % 64 == 0 and group = 64 * 2^j use the
 // large-tile kernel with the largest tile that still yields a full wave of
 // workgroups; anything else (fp32, K % 64 != 0, tiny problems) the generic
@@ -881,7 +945,16 @@ void launch_mode(const GemmProblem& p) {
   auto tiles = [&](int bm, int bn) { return ((p.rows + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
   int splits = 1;
   if (cfg == 0) {
-    if (tiles(256, 256) >= 240) cfg = 2;
+    // Whole waves of workgroups over the CUs matter at these sizes: 256 x 224
+    // tiles (16x16 MFMA blocks) when they fill the last wave better than
+    // 256 x 256, e.g. 2048 x 14336 = 512 tiles (two full waves on 256 CUs)
+    // instead of 448 (1.75).
+    auto fill = [&](int64_t t) {
+      const int64_t cus = num_cus();
+      return (double)t / (double)(((t + cus - 1) / cus) * cus);
+    };
+    if (tiles(256, 224) >= 240 && fill(tiles(256, 224)) > fill(tiles(256, 256)) + 0.05) cfg = 9;
+    else if (tiles(256, 256) >= 240) cfg = 2;
     else if (tiles(128, 256) >= 200) cfg = 3;
     else {
       cfg = 4;  // 128 x 128 tiles, two workgroups per CU
@@ -904,6 +977,7 @@ void launch_mode(const GemmProblem& p) {
       case 6: return launch_big<MODE, ST, 256, 128, 4, 2>(p, splits);
       case 7: return launch_big<MODE, ST, 256, 256, 2, 2>(p, splits);
       case 8: return launch_big<MODE, ST, 64, 256, 1, 8>(p, splits);
+      case 9: return launch_big<MODE, ST, 256, 224, 4, 2, 16>(p, splits);
       default: break;
     }
   }

@@ -274,3 +274,20 @@ def test_repeated_calls_bit_identical(dev, M):
     for _ in range(3):
         b = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, x_dt, "f16"))
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9])
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("x_dt", ["f16", "bf16"])
+def test_prefill_every_tile_configuration(dev, monkeypatch, tile, splits, x_dt):
+    """Every prefill kernel configuration (tile shape, MFMA shape, split-K),
+    forced through the tuning overrides, on a shape ragged in M and N for all
+    of them, with bias."""
+    monkeypatch.setenv("AWQ_GEMM_TILE", str(tile))
+    monkeypatch.setenv("AWQ_GEMM_SPLITS", str(splits))
+    M, K, N, g = 300, 512, 672, 128
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32")
+    got = to_host(y)
+    assert np.isfinite(got).all()
+    assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_MFMA
