@@ -162,6 +162,24 @@ def main():
         steps = 50 if args.only is None else max(10, args.steps // 100)
         ms, calls, wall = graph_time(pre, 10, 5, steps)
         out["prefill"] = dict(ms=ms, calls=calls, wall_s=wall, tflops=pf_flops / (ms * 1e-3) / 1e12)
+        if args.only is None:
+            # Context, not a roofline: the library dense fp16 GEMM (torch ->
+            # hipBLASLt) of the same shape on unquantised f16 weights, W given
+            # as [N, K] (its faster layout). The fused kernel additionally
+            # dequantises W on the fly.
+            wd = torch.randn((N, K), dtype=torch.float16, device=dev,
+                             generator=torch.Generator(device=dev).manual_seed(7))
+            yd = torch.empty((PM, N), dtype=torch.float16, device=dev)
+
+            def dense(i):
+                torch.matmul(xp, wd.t(), out=yd)
+
+            try:
+                dms, _, _ = graph_time(dense, 10, 5, 50)
+                out["prefill"]["dense_tflops"] = pf_flops / (dms * 1e-3) / 1e12
+            except RuntimeError as e:  # informational only: never fail the bench on it
+                print(f"dense comparison skipped: {e}", file=sys.stderr)
+            del wd, yd
 
     # ---------------- dequantize K=14336, N=4096, g64 -------------------------------------
     DK, DN, DG = 14336, 4096, 64
@@ -255,6 +273,8 @@ def main():
                                              "frac": round(p["tflops"] / FP16_MFMA_PEAK_TFLOPS, 4),
                                              "traffic": traffic.get("prefill_m2048_4096x14336")},
                                 "dtype": "f16 in, fp32 accumulate, f16 out", "calls": p["calls"]}
+        if "dense_tflops" in p:
+            res["prefill_m2048"]["dense_fp16_library_gemm_tflops"] = round(p["dense_tflops"], 2)
     if "dequant" in out:
         q = out["dequant"]
         res["dequant_k14336_n4096_g64"] = {
