@@ -30,6 +30,7 @@
 // (q - z) * s, the value the reference computes with F = f16. Odd packed
 // lanes (high nibble of the byte) take one extra shift.
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <type_traits>
 
@@ -74,6 +75,7 @@ struct GemmArgs {
   int32_t M, K, N, group;
   int32_t tiles_m, tiles_n;
   int32_t swizzled_tiles;  // leading tiles covered by the XCD mapping (multiple of 8)
+  int32_t group_m;         // row tiles per raster group (large-tile kernel)
   int32_t grp_shift;       // large-tile kernel: group = 64 << grp_shift
   // Large-tile kernel split-K (grid.y = splits): workgroup y covers stages
   // [y * stages_per_split, ...); partials [splits][M][N] and one arrival
@@ -440,8 +442,15 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     const int per_xcd = a.swizzled_tiles >> 3;
     t = (t & 7) * per_xcd + (t >> 3);
   }
-  const int tile_m = t % a.tiles_m;
-  const int tile_n = t / a.tiles_m;
+  // Raster in groups of group_m row tiles, row tiles fastest inside a group:
+  // the tiles an XCD runs at one time then cover a few row tiles by several
+  // column tiles, so X and W are each fetched into its L2 by few of them.
+  const int gsz = a.group_m * a.tiles_n;
+  const int grp = t / gsz;
+  const int gm = min(a.group_m, a.tiles_m - grp * a.group_m);
+  const int r = t - grp * gsz;
+  const int tile_m = grp * a.group_m + r % gm;
+  const int tile_n = r / gm;
   const int m0 = tile_m * BM, n0 = tile_n * BN;
   const int np = a.N >> 3;
   // K range of this workgroup: all of K, or its split's run of stages.
@@ -831,6 +840,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 }
 
+int64_t num_cus();
+
+// Row tiles per raster group. An XCD runs about CUs/8 tiles at once; with a
+// rows by b columns of them (a*b fixed) it fetches a*BM + b*BN/4 row-bytes of
+// X and W per K step (f16 X, 4-bit W), least near a = sqrt(CUs/8 * BN / (4 BM)).
+int raster_group_m(int tiles_m, int bm, int bn) {
+  if (const char* e = std::getenv("AWQ_GEMM_GROUP_M")) {
+    const int v = std::atoi(e);
+    if (v > 0) return std::min(v, tiles_m);
+  }
+  const double conc = (double)std::max<int64_t>(1, num_cus() / 8);
+  const double best = std::sqrt(conc * bn / (4.0 * bm));
+  int a = 1;
+  while (a * 2 <= tiles_m && a * 2 <= best * 1.41421356) a *= 2;
+  return a;
+}
+
 template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS = 32>
 void launch_big(const GemmProblem& p, int splits = 1) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
@@ -852,6 +878,7 @@ void launch_big(const GemmProblem& p, int splits = 1) {
   a.tiles_n = (int)((p.N + BN - 1) / BN);
   const int tiles = a.tiles_m * a.tiles_n;
   a.swizzled_tiles = tiles & ~7;
+  a.group_m = raster_group_m(a.tiles_m, BM, BN);
   a.grp_shift = __builtin_ctzll(p.group / kBK);
   const int total_stages = (int)(p.K / kBK);
   // Partials are addressed through a 32-bit buffer range.

@@ -291,3 +291,18 @@ def test_prefill_every_tile_configuration(dev, monkeypatch, tile, splits, x_dt):
     got = to_host(y)
     assert np.isfinite(got).all()
     assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_MFMA
+
+
+@pytest.mark.parametrize("group_m", [1, 2, 3, 5])
+def test_prefill_tile_raster_groups(dev, monkeypatch, group_m):
+    """The grouped tile order of the large-tile kernel covers every output
+    tile once, including a last group with fewer row tiles than the others
+    (7 row tiles of 128) and tiles past the XCD-mapped multiple of 8."""
+    monkeypatch.setenv("AWQ_GEMM_TILE", "4")
+    monkeypatch.setenv("AWQ_GEMM_GROUP_M", str(group_m))
+    M, K, N, g = 800, 256, 1152, 64
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt="f16", bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f16", "f16", "f32")
+    got = to_host(y)
+    assert np.isfinite(got).all()
+    assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, "f16", "f16")) <= TOL_MFMA
