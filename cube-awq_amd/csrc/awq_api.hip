@@ -470,6 +470,15 @@ int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t
   });
 }
 
+int awq_validate_gemm(int64_t M, int64_t K, int64_t N, int64_t group_size) {
+  return guarded([&] {
+    AWQ_ASSERT(M >= 0 && K >= 0 && N >= 0, "shape sizes must be non-negative");
+    awq_shape_config s = awq_shape_config_new(M, N, K, select_tile_m(M), select_tile_n(N), kInnerK);
+    if (M <= kDecodeMThreshold) validate_decode(s, group_size);
+    else validate_prefill(s, group_size);
+  });
+}
+
 int awq_dequantize(const uint32_t* qweight, const uint32_t* qzeros, const void* scales,
                    int32_t s_t, void* out, int32_t o_t, int64_t K, int64_t N,
                    int64_t group_size, int32_t order, void* stream) {

@@ -22,41 +22,76 @@ SEED_BASE = 0xA77A0000
 TID_X, TID_QWEIGHT, TID_QZEROS, TID_SCALES, TID_BIAS = range(5)
 
 
+_BLOCK = 1 << 17  # draws per block: keeps the uint64 temporaries in cache
+
+
+def _draws(seed, start, count):
+    """Draws start .. start+count-1 (0-based) of the stream seeded with `seed`."""
+    with np.errstate(over="ignore"):
+        z = np.arange(start + 1, start + count + 1, dtype=np.uint64)
+        z *= _GOLDEN
+        z += np.uint64(seed)
+        t = z >> np.uint64(30)
+        z ^= t
+        z *= _M1
+        np.right_shift(z, np.uint64(27), out=t)
+        z ^= t
+        z *= _M2
+        np.right_shift(z, np.uint64(31), out=t)
+        z ^= t
+        return z
+
+
 def splitmix64(seed, n):
     """First n draws of SplitMix64 seeded with `seed`, as uint64."""
-    with np.errstate(over="ignore"):
-        i = np.arange(1, n + 1, dtype=np.uint64)
-        z = np.uint64(seed) + i * _GOLDEN
-        z = (z ^ (z >> np.uint64(30))) * _M1
-        z = (z ^ (z >> np.uint64(27))) * _M2
-        return z ^ (z >> np.uint64(31))
+    out = np.empty(n, dtype=np.uint64)
+    for s in range(0, n, _BLOCK):
+        out[s:s + _BLOCK] = _draws(seed, s, min(_BLOCK, n - s))
+    return out
 
 
 def packed_nibbles(tensor_id, rows, words_per_row):
     """uint32 [rows, words_per_row] of uniform 4-bit nibbles."""
     n = rows * words_per_row
-    nib = (splitmix64(SEED_BASE + tensor_id, n * 8) >> np.uint64(60)).astype(np.uint32)
-    nib = nib.reshape(n, 8)
-    shifts = (np.arange(8, dtype=np.uint32) * 4)[None, :]
-    words = np.bitwise_or.reduce(nib << shifts, axis=1).astype(np.uint32)
-    return words.reshape(rows, words_per_row)
+    out = np.empty(n, dtype=np.uint32)
+    wb = _BLOCK // 8
+    for s in range(0, n, wb):
+        e = min(n, s + wb)
+        z = _draws(SEED_BASE + tensor_id, 8 * s, 8 * (e - s))
+        z >>= np.uint64(60)
+        nib = z.astype(np.uint32).reshape(-1, 8)
+        w = nib[:, 0].copy()
+        for j in range(1, 8):
+            w |= nib[:, j] << np.uint32(4 * j)
+        out[s:e] = w
+    return out.reshape(rows, words_per_row)
 
 
 def uniform(tensor_id, shape, a, b, dtype=np.float32):
     n = int(np.prod(shape))
-    u = (splitmix64(SEED_BASE + tensor_id, n) >> np.uint64(40)).astype(np.float64) / float(1 << 24)
-    return _round_to(a + (b - a) * u, dtype).reshape(shape)
+    out = np.empty(n, dtype=np.uint16 if dtype == "bfloat16" else dtype)
+    for s in range(0, n, _BLOCK):
+        c = min(_BLOCK, n - s)
+        u = (_draws(SEED_BASE + tensor_id, s, c) >> np.uint64(40)).astype(np.float64) / float(1 << 24)
+        out[s:s + c] = _round_to(a + (b - a) * u, dtype)
+    return out.reshape(shape)
 
 
 def normal(tensor_id, shape, dtype=np.float32):
     n = int(np.prod(shape))
-    pairs = (n + 1) // 2
-    d = splitmix64(SEED_BASE + tensor_id, 2 * pairs).reshape(pairs, 2)
-    u1 = ((d[:, 0] >> np.uint64(11)).astype(np.float64) + 1.0) / float(1 << 53)
-    u2 = (d[:, 1] >> np.uint64(11)).astype(np.float64) / float(1 << 53)
-    r = np.sqrt(-2.0 * np.log(u1))
-    z = np.stack([r * np.cos(2 * np.pi * u2), r * np.sin(2 * np.pi * u2)], axis=1).reshape(-1)[:n]
-    return _round_to(z, dtype).reshape(shape)
+    out = np.empty(n, dtype=np.uint16 if dtype == "bfloat16" else dtype)
+    pb = _BLOCK // 2
+    for s in range(0, n, 2 * pb):  # s: first value of the block (even)
+        c = min(2 * pb, n - s)
+        pairs = (c + 1) // 2
+        d = _draws(SEED_BASE + tensor_id, s, 2 * pairs).reshape(pairs, 2)
+        u1 = ((d[:, 0] >> np.uint64(11)).astype(np.float64) + 1.0) / float(1 << 53)
+        u2 = (d[:, 1] >> np.uint64(11)).astype(np.float64) / float(1 << 53)
+        r = np.sqrt(-2.0 * np.log(u1))
+        t = 2 * np.pi * u2
+        z = np.stack([r * np.cos(t), r * np.sin(t)], axis=1).reshape(-1)[:c]
+        out[s:s + c] = _round_to(z, dtype)
+    return out.reshape(shape)
 
 
 def _round_to(v64, dtype):

@@ -120,6 +120,13 @@ int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t
              const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
              int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream);
 
+/* Host-only check of an awq_gemm problem: the same shape validation awq_gemm
+ * applies (the module's constraints through validate_launch_params_impl,
+ * src/kernel/awq_kernel_gemm.rs:89-171, with the M <= 8 decode split of :691),
+ * without touching the GPU. 0 if awq_gemm would accept the shapes, else the
+ * error code with awq_last_error() set to the reference's panic text. */
+int awq_validate_gemm(int64_t M, int64_t K, int64_t N, int64_t group_size);
+
 /* Pointer-level dequantize: out[K, N] in o_t from scales in s_t (s_t == o_t is
  * the reference's single-F case), either nibble order. N % 32 == 0, K % g == 0. */
 int awq_dequantize(const uint32_t* qweight, const uint32_t* qzeros, const void* scales,

@@ -12,7 +12,7 @@ import torch
 
 import awq_oracle as oracle
 import cube_awq
-from cube_awq import AWQGEMMLinear, ShapeConfig, _lib
+from cube_awq import AWQGEMMLinear, ShapeConfig, _lib, synth
 from conftest import load_golden
 from helpers import TORCH_OF, host_f32, make_problem, to_device, to_host
 
@@ -212,6 +212,38 @@ def test_prefill_m2048_gate_up_sampled_rows(dev):
     rows = np.r_[0:16, 1000:1016, 2032:2048]
     got = host_f32(to_host(y)[rows], "f16")
     assert oracle.rel_l2(got, _ref64(x[rows], qw, qz, sc, None, g, "f16", "f16")) <= TOL_MFMA
+
+
+# Llama-3-70B projections (8192 -> 8192, 8192 -> 1024, 8192 -> 28672,
+# 28672 -> 8192), g128, fp16 activations N(0,1) and f16 scales, f16 output,
+# from decode (M = 1, 8) to prefill (M = 128 .. 4096). Outputs are checked on
+# all rows for M <= 8 and on 8 sampled rows otherwise (the f64 oracle costs
+# K*N per row).
+_SHAPES_70B = [(8192, 8192), (8192, 1024), (8192, 28672), (28672, 8192)]
+_CASES_70B = [(K, N, M) for (K, N) in _SHAPES_70B for M in (1, 8, 128, 1024, 4096)]
+_weights_70b = {}
+
+
+def _weights_for(K, N, g):
+    if (K, N) not in _weights_70b:
+        _weights_70b.clear()  # one shape's weights held at a time
+        _, qw, qz, sc, _ = make_problem(1, K, N, g, x_dt="f16", s_dt="f16")
+        _weights_70b[(K, N)] = (qw, qz, sc)
+    return _weights_70b[(K, N)]
+
+
+@pytest.mark.parametrize("K,N,M", _CASES_70B)
+def test_llama70b_projection_shapes(dev, K, N, M):
+    g = 128
+    qw, qz, sc = _weights_for(K, N, g)
+    x = synth.normal(synth.TID_X, (M, K), np.float16)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f16", "f16", "f16"))
+    rows = np.arange(M) if M <= 8 else np.r_[0:3, M // 2:M // 2 + 2, M - 3:M]
+    got = host_f32(y[rows], "f16")
+    assert np.isfinite(got).all()
+    ref = _ref64(x[rows], qw, qz, sc, None, g, "f16", "f16")
+    # f16 output: one rounding of a value of relative size ~2^-11.
+    assert oracle.rel_l2(got, ref) <= (1e-3 if M <= 8 else TOL_MFMA)
 
 
 @pytest.mark.parametrize("M,K,N,g", [(9, 256, 96, 64), (100, 512, 224, 128), (130, 4096, 1024, 128),

@@ -295,3 +295,27 @@ def test_last_error_cleared_on_success():
     import ctypes
     assert L.awq_validate_launch_params(ctypes.byref(s), 32) == 0
     assert L.awq_last_error().decode() == ""
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 96, 32, 64), (1, 64, 48, 64), (1, 128, 32, 32), (1, 192, 32, 128),
+                                     (64, 96, 32, 64), (64, 64, 48, 64), (64, 128, 32, 0), (9, 64, 40, 64),
+                                     (0, 64, 32, 64), (8, 4096, 14336, 96)])
+def test_validate_gemm_matches_awq_gemm(M, K, N, g):
+    """awq_validate_gemm runs awq_gemm's shape checks alone: same result code
+    and message, with no device pointer needed."""
+    L = cube_awq.lib()
+    rc_v = L.awq_validate_gemm(M, K, N, g)
+    msg_v = L.awq_last_error().decode()
+    rc_g = L.awq_gemm(None, _lib.AWQ_F32, None, None, None, _lib.AWQ_F32, None, 0, None,
+                      _lib.AWQ_F32, M, K, N, g, None)
+    msg_g = L.awq_last_error().decode()
+    assert rc_v == rc_g == _lib.AWQ_ERR_INVALID
+    assert msg_v == msg_g and msg_v
+
+
+@pytest.mark.parametrize("M,K,N,g", [(1, 4096, 14336, 128), (8, 4096, 4096, 128), (2048, 4096, 14336, 128),
+                                     (4096, 28672, 8192, 64), (9, 64, 32, 64)])
+def test_validate_gemm_accepts_module_shapes(M, K, N, g):
+    L = cube_awq.lib()
+    assert L.awq_validate_gemm(M, K, N, g) == 0
+    assert L.awq_last_error().decode() == ""
