@@ -438,18 +438,23 @@ int awq_dequantize_native(const awq_tensor_ref* q_weight, const awq_tensor_ref* 
 
 // Module-level forward (AWQGEMMLinear::forward, src/modules/awq_gemm.rs:146-232)
 // on plain pointers: tile choice by select_tile_m/n, INNER_K = 64.
-int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
-             const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
-             int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream) {
+static int gemm_entry(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                      const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                      int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                      int32_t order, void* stream) {
   return guarded([&] {
     AWQ_ASSERT(M >= 0 && K >= 0 && N >= 0, "shape sizes must be non-negative");
     awq_shape_config s = awq_shape_config_new(M, N, K, select_tile_m(M), select_tile_n(N), kInnerK);
     if (M <= kDecodeMThreshold) validate_decode(s, group_size);
     else validate_prefill(s, group_size);
+    AWQ_ASSERT(order == AWQ_ORDER_AUTOAWQ || order == AWQ_ORDER_SEQUENTIAL,
+               "order must be AWQ_ORDER_AUTOAWQ or AWQ_ORDER_SEQUENTIAL");
     check_float_dtype(x_t, "input");
     check_float_dtype(s_t, "scales");
     check_float_dtype(y_t, "output");
     if (bias) check_float_dtype(b_t, "bias");
+    if (order == AWQ_ORDER_SEQUENTIAL)
+      AWQ_ASSERT(s_t == x_t, "sequential-order GEMM needs scales in the input dtype");
     GemmProblem p{};
     p.x = x;
     p.xt = x_t;
@@ -465,9 +470,25 @@ int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t
     p.K = K;
     p.N = N;
     p.group = group_size;
+    p.order = order;
     p.stream = static_cast<hipStream_t>(stream);
     run_gemm(p, M);
   });
+}
+
+int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+             const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+             int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream) {
+  return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
+                    AWQ_ORDER_AUTOAWQ, stream);
+}
+
+int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                     const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                     int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                     int32_t order, void* stream) {
+  return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
+                    order, stream);
 }
 
 int awq_validate_gemm(int64_t M, int64_t K, int64_t N, int64_t group_size) {

@@ -143,6 +143,7 @@ struct GemmProblem {
   int32_t yt;
   int64_t rows;  // rows to compute and write (m_valid)
   int64_t K, N, group;
+  int32_t order;  // AWQ_ORDER_AUTOAWQ (awq_gemm) or AWQ_ORDER_SEQUENTIAL (AWQLinear's weights)
   hipStream_t stream;
 };
 

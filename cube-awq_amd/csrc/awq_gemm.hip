@@ -107,6 +107,11 @@ __device__ __forceinline__ uint32_t deq_pair_f16(uint32_t w0, uint32_t w1, uint3
   return __builtin_bit_cast(uint32_t, r);
 }
 
+// Packed lane holding column c of a pack: AutoAWQ interleave, or lane c in
+// sequential order (the order AWQLinear's weights use).
+template <bool SEQ>
+__host__ __device__ constexpr int lane_of_col(int c) { return SEQ ? c : awq_lane_of_col(c); }
+
 template <int MODE, int BM, int BN, int WGM, int WGN>
 struct Tile {
   typedef typename ModeT<MODE>::T T;
@@ -126,7 +131,7 @@ struct Tile {
 // Hint for the register allocator: the 256x256 tile runs one workgroup per CU.
 constexpr int min_blocks(int tile_elems) { return tile_elems >= 256 * 256 ? 1 : 2; }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ>
 __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kernel(GemmArgs a) {
   using C = Tile<MODE, BM, BN, WGM, WGN>;
   typedef typename C::T T;
@@ -229,7 +234,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
       uint32_t out[8][2];
 #define AWQ_DEQ_COL(CC)                                                                \
   {                                                                                     \
-    constexpr int L = awq_lane_of_col(CC);                                              \
+    constexpr int L = lane_of_col<SEQ>(CC);                                             \
     const uint32_t z = (zw >> (4 * L)) & 0xFu;                                          \
     const f16_t zf = (f16_t)(1024.0f + (float)z);                                       \
     const f16_t sf = (f16_t)to_f32(srow[CC]);                                           \
@@ -249,7 +254,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
       // arithmetic), then one rounding to T.
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const int L = awq_lane_of_col(c);
+        const int L = lane_of_col<SEQ>(c);
         const int z = (int)((zw >> (4 * L)) & 0xFu);
         const float sv = to_f32(srow[c]);
         T v[4];
@@ -424,7 +429,7 @@ struct BigTile {
   static_assert(kWTM % MS == 0 && kWTN % MS == 0, "wave tile must be whole MFMA blocks");
 };
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   using S = typename Elem<ST>::type;
@@ -539,7 +544,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // buf: LDS column 8 wp + c, whose slot is that of column 8 wp flipped by c.
   auto deq_store_col = [&](const WRegs& r_, int c, int buf) {
     uint32_t dq[RW / 2];
-    const int L = awq_lane_of_col(c);
+    const int L = lane_of_col<SEQ>(c);
     const uint32_t zw = r_.z;
     if constexpr (MODE == MODE_F16) {
       // Nibbles of packed lane L as f16 magic numbers (1024 + q or 64 + q),
@@ -857,8 +862,8 @@ int raster_group_m(int tiles_m, int bm, int bn) {
   return a;
 }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS = 32>
-void launch_big(const GemmProblem& p, int splits = 1) {
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ>
+void launch_big(const GemmProblem& p, int splits) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   GemmArgs a{};
   a.x = p.x;
@@ -893,17 +898,17 @@ void launch_big(const GemmProblem& p, int splits = 1) {
   }
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kSmem),
               "hipFuncSetAttribute(gemm_big)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS>), dim3(tiles, a.splits),
+  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ>), dim3(tiles, a.splits),
                      dim3(C::kThreads), C::kSmem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ>
 void launch_cfg(const GemmProblem& p) {
   using C = Tile<MODE, BM, BN, WGM, WGN>;
   GemmArgs a{};
@@ -928,12 +933,12 @@ void launch_cfg(const GemmProblem& p) {
   const size_t smem = C::kSmem;
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
               "hipFuncSetAttribute(gemm)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<MODE, ST, BM, BN, WGM, WGN>), dim3(tiles), dim3(C::kThreads),
+  hipLaunchKernelGGL((gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ>), dim3(tiles), dim3(C::kThreads),
                      smem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
@@ -961,7 +966,7 @@ int64_t num_cus() {
 // large-tile kernel with the largest tile that still yields a full wave of
 // workgroups; anything else (fp32, K % 64 != 0, tiny problems) the generic
 // 128x128 kernel.
-template <int MODE, int ST>
+template <int MODE, int ST, bool SEQ>
 void launch_mode(const GemmProblem& p) {
   int cfg = env_int("AWQ_GEMM_TILE", 0);  // tuning override: 1 generic, 2.. large tiles
   const int64_t gs = p.group / kBK;
@@ -998,25 +1003,33 @@ void launch_mode(const GemmProblem& p) {
   if (int v = env_int("AWQ_GEMM_SPLITS", 0); v >= 1) splits = v;
   if constexpr (MODE != MODE_F32) {
     switch (cfg) {
-      case 2: return launch_big<MODE, ST, 256, 256, 2, 4>(p, splits);
-      case 3: return launch_big<MODE, ST, 128, 256, 2, 4>(p, splits);
-      case 4: return launch_big<MODE, ST, 128, 128, 2, 2>(p, splits);
-      case 6: return launch_big<MODE, ST, 256, 128, 4, 2>(p, splits);
-      case 7: return launch_big<MODE, ST, 256, 256, 2, 2>(p, splits);
-      case 8: return launch_big<MODE, ST, 64, 256, 1, 8>(p, splits);
-      case 9: return launch_big<MODE, ST, 256, 224, 4, 2, 16>(p, splits);
+      case 2: return launch_big<MODE, ST, 256, 256, 2, 4, 32, SEQ>(p, splits);
+      case 3: return launch_big<MODE, ST, 128, 256, 2, 4, 32, SEQ>(p, splits);
+      case 4: return launch_big<MODE, ST, 128, 128, 2, 2, 32, SEQ>(p, splits);
+      case 6: return launch_big<MODE, ST, 256, 128, 4, 2, 32, SEQ>(p, splits);
+      case 7: return launch_big<MODE, ST, 256, 256, 2, 2, 32, SEQ>(p, splits);
+      case 8: return launch_big<MODE, ST, 64, 256, 1, 8, 32, SEQ>(p, splits);
+      case 9: return launch_big<MODE, ST, 256, 224, 4, 2, 16, SEQ>(p, splits);
       default: break;
     }
   }
-  launch_cfg<MODE, ST, 128, 128, 2, 2>(p);
+  launch_cfg<MODE, ST, 128, 128, 2, 2, SEQ>(p);
 }
 
 template <int MODE>
 void launch_st(const GemmProblem& p) {
+  if (p.order == AWQ_ORDER_SEQUENTIAL) {
+    // Sequential order (AWQLinear): scales in the activations' dtype, as the
+    // reference's single float type F has them.
+    constexpr int kST = MODE == MODE_F16 ? AWQ_F16 : MODE == MODE_BF16 ? AWQ_BF16 : AWQ_F32;
+    AWQ_ASSERT(p.st == kST, "sequential-order GEMM needs scales in the input dtype");
+    launch_mode<MODE, kST, true>(p);
+    return;
+  }
   switch (p.st) {
-    case AWQ_F32: launch_mode<MODE, AWQ_F32>(p); break;
-    case AWQ_F16: launch_mode<MODE, AWQ_F16>(p); break;
-    default: launch_mode<MODE, AWQ_BF16>(p); break;
+    case AWQ_F32: launch_mode<MODE, AWQ_F32, false>(p); break;
+    case AWQ_F16: launch_mode<MODE, AWQ_F16, false>(p); break;
+    default: launch_mode<MODE, AWQ_BF16, false>(p); break;
   }
 }
 

@@ -54,6 +54,7 @@ struct GemvArgs {
   int32_t rows;       // valid rows (<= MT)
   int32_t K, N, group;
   int32_t splits;
+  int32_t seq;        // sequential nibble order (packed lane j = column j)
 };
 
 template <int XT>
@@ -240,9 +241,22 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
   }
 
   // ---- fold zero point and scale (zero points in the weights' scaled domain) ----
+  // Accumulator slot c holds the packed lane that split_word puts there: lane
+  // kAwqLaneOfCol[c], which is column c in AutoAWQ order and column
+  // seq_col(c) = (c >> 1) + 4 (c & 1) in sequential order. Zero points come
+  // through the same masks; scales (and, below, outputs) are per column, so in
+  // sequential order they are permuted to slot order (once per wave).
   float zl[8], sl[8];
   word_values(zw, zl);
   scales_to_f32(sraw, a.st, sl);
+  const bool seq = a.seq != 0;
+  {
+    float t[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) t[c] = seq ? sl[(c >> 1) + 4 * (c & 1)] : sl[c];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) sl[c] = t[c];
+  }
   float acc[MT][8];
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
@@ -260,9 +274,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
   // ---- sum the waves of the workgroup (fixed order) ------------------------------
 #pragma unroll
   for (int m = 0; m < MT; ++m) {
+    float o[8];  // column order: column j is slot j (AutoAWQ) or slot 2 (j & 3) + (j >> 2)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = seq ? acc[m][2 * (j & 3) + (j >> 2)] : acc[m][j];
     float4* dst = reinterpret_cast<float4*>(&red[wave][m][lane * 8]);
-    dst[0] = make_float4(acc[m][0], acc[m][1], acc[m][2], acc[m][3]);
-    dst[1] = make_float4(acc[m][4], acc[m][5], acc[m][6], acc[m][7]);
+    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
   }
   __syncthreads();
   constexpr int kOut = MT * kChunkCols;
@@ -372,6 +389,7 @@ void launch_cfg(const GemmProblem& p) {
   a.N = (int32_t)p.N;
   a.group = (int32_t)p.group;
   a.splits = splits;
+  a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MT * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);

@@ -9,9 +9,13 @@ Same constructors, builder methods, parameter shapes, `group_size()`,
     reference launches a separate elementwise add, src/modules/awq_gemm.rs:225-228).
   * M is a runtime argument of one compiled kernel; the reference JIT-compiles
     a kernel per distinct M (M is part of its comptime ShapeConfig).
-  * AWQLinear.forward's matmul half is the third-party GEMM of the framework
-    holding the tensors (torch here, Burn's autotuned matmul in the
-    reference, src/modules/awq_dequantize.rs:99-105).
+  * AWQLinear.forward (dequantize, then Burn's autotuned matmul in the
+    reference, src/modules/awq_dequantize.rs:74-108) runs as one fused
+    dequant-GEMM launch in sequential nibble order when the shapes meet the
+    fused kernels' constraints (those of AWQGEMMLinear: K % 64, N % 32,
+    g % 64, g >= 64) and the scales share the input's dtype; other shapes
+    (e.g. the reference's g = 2 test layer) take dequantize() and torch's
+    matmul, the reference's own two steps.
 Parameters are plain torch tensors on the module's device: qweight/qzeros
 int32 (AutoAWQ checkpoints store int32; uint32 is accepted too), scales and
 bias in the backend float type.
@@ -161,12 +165,36 @@ class AWQLinear:
         return dequantize_awq(self.qweight, self.qzeros, self.scales, self.group_size(), stream)
 
     def forward(self, input, stream=None):
-        """dequantize() then a library matmul, as src/modules/awq_dequantize.rs:74-108.
-        Like the reference (whose 2-D weight meets a D-rank input in Burn's
-        matmul), a rank other than 2 is rejected (here before any work is queued)."""
+        """input [M, K] -> [M, N] = input @ dequantize(), as
+        src/modules/awq_dequantize.rs:74-108. Like the reference (whose 2-D
+        weight meets a D-rank input in Burn's matmul), a rank other than 2 is
+        rejected (here before any work is queued)."""
         if input.dim() != 2:
             raise Panic(f"RankMismatch {{ lhs: {input.dim()}, rhs: 2 }}")
+        m, k = input.shape
+        n = self.scales.shape[-1]
+        if self._fusable(input, m, k, n):
+            x = input if input.is_contiguous() and input.data_ptr() % 16 == 0 else input.clone()
+            out = torch.empty((m, n), dtype=input.dtype, device=input.device)
+            check(lib().awq_gemm_ordered(
+                x.data_ptr(), _lib.awq_dtype(x),
+                self.qweight.data_ptr(), self.qzeros.data_ptr(),
+                self.scales.data_ptr(), _lib.awq_dtype(self.scales),
+                None, _lib.AWQ_F32, out.data_ptr(), _lib.awq_dtype(out),
+                m, k, n, self.group_size(), _lib.AWQ_ORDER_SEQUENTIAL,
+                stream_ptr(stream, input.device)))
+            return out
         weight = self.dequantize(stream)
         return torch.matmul(input, weight.to(input.dtype))
+
+    def _fusable(self, input, m, k, n):
+        """True when the fused sequential-order launch takes this problem."""
+        return (input.is_cuda and input.dtype == self.scales.dtype and m > 0
+                and k == self.qweight.shape[0] and self.qweight.shape[-1] * 8 == n
+                and self.qweight.dtype in (torch.int32, torch.uint32)
+                and self.qzeros.dtype in (torch.int32, torch.uint32)
+                and self.scales.is_contiguous() and self.qweight.is_contiguous()
+                and self.qzeros.is_contiguous()
+                and lib().awq_validate_gemm(m, k, n, self.group_size()) == 0)
 
     __call__ = forward

@@ -120,6 +120,17 @@ int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t
              const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
              int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream);
 
+/* awq_gemm with the nibble order of qweight/qzeros as a parameter.
+ * AWQ_ORDER_AUTOAWQ is awq_gemm. AWQ_ORDER_SEQUENTIAL is AWQLinear's layout:
+ * the reference's AWQLinear::forward (src/modules/awq_dequantize.rs:74-108)
+ * dequantizes in that order (src/kernel/awq_kernel.rs:23-61) and then runs a
+ * matmul; here the two are one fused launch, with scales in the input dtype
+ * (the reference's single F). Same shape constraints as awq_gemm. */
+int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                     const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                     int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                     int32_t order, void* stream);
+
 /* Host-only check of an awq_gemm problem: the same shape validation awq_gemm
  * applies (the module's constraints through validate_launch_params_impl,
  * src/kernel/awq_kernel_gemm.rs:89-171, with the M <= 8 decode split of :691),
