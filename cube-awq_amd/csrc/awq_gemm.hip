@@ -1,34 +1,39 @@
 // awq_gemm.hip -- prefill path (M > 8) of the fused AWQ dequant-GEMM for gfx950.
 //
-// Y[M, N] = X[M, K] . W[K, N], W[k, n] = (q - z) * s (AutoAWQ nibble order),
-// the operation of the reference's gemm_awq (src/kernel/awq_kernel_gemm.rs:
-// 181-439), which runs it as scalar vector-FMA in the activation type. Here it
-// runs on CDNA4 matrix cores with fp32 accumulation:
-//   f16  activations: v_mfma_f32_32x32x16_f16, W dequantised to f16
-//   bf16 activations: v_mfma_f32_32x32x16_bf16, W dequantised to bf16
-//   f32  activations: v_mfma_f32_32x32x2_f32, W dequantised in f32 exactly as
-//                     the reference's F = f32 kernel does
+// Y[M, N] = X[M, K] . W[K, N], W[k, n] = (q - z) * s, the operation of the
+// reference's gemm_awq (src/kernel/awq_kernel_gemm.rs:181-439), which runs it
+// as scalar vector-FMA in the activation type. Here it runs on CDNA4 matrix
+// cores with fp32 accumulation. Nibbles are read in AutoAWQ order, or in
+// sequential order (SEQ, the layout AWQLinear's weights use): the order only
+// changes which packed lane a column is taken from.
 //
-// Tiling (template BM x BN, 2*BN threads): a workgroup of WGM x WGN waves owns
-// a BM x BN tile of Y (each wave a (BM/WGM) x (BN/WGN) block of 32 x 32 MFMA
-// tiles) and walks K in 64-row stages. Per stage it loads the X tile
-// (row-major) and the packed 64 x BN/8-word W tile, dequantises W in
-// registers (each thread 4 rows x 8 columns) and writes it to LDS transposed,
-// n-major with k contiguous, so that both MFMA operands are single 16-byte
-// LDS reads (lane l of a 32x32xK MFMA needs 8 consecutive k of one row of X
-// and of one column of W). LDS is double buffered: global loads of stage s+1
-// are in flight while stage s feeds the matrix cores, one barrier per stage.
-// Configurations: 256x256 (8 waves, 147 KB LDS, one workgroup per CU) for
-// large problems; 128x128 (4 waves) for small ones and the fp32 path. Tile
-// indices are mapped so that the tiles one XCD runs share W columns.
-//
-// f16 dequant (2.25 VALU ops per weight): for column c (packed lane L) and
-// rows r, r+1, one v_perm_b32 gathers the byte holding lane L of both words
-// into the two 16-bit halves, one v_and_or_b32 turns the nibbles into f16
-// 1024+q (0x6400 | q), one v_pk_add_f16 subtracts 1024+z exactly and one
-// v_pk_mul_f16 applies the scale: the result is the correctly rounded f16 of
-// (q - z) * s, the value the reference computes with F = f16. Odd packed
-// lanes (high nibble of the byte) take one extra shift.
+// gemm_big_kernel (f16/bf16 activations, K % 64 == 0, group = 64 * 2^j):
+//  * A workgroup of WGM x WGN waves owns a BM x BN tile of Y (256x224,
+//    256x256, 128x256, 128x128, ...; v_mfma_f32_32x32x16 or, for 256x224,
+//    v_mfma_f32_16x16x32 blocks) and walks its K range in 64-row stages.
+//  * X goes global -> LDS directly (buffer_load_dwordx4 ... lds, no VGPR
+//    staging), two stages ahead in three LDS buffers when they fit. Each LDS
+//    row is 128 bytes of eight 16-byte granules at slot g ^ swz(row), which
+//    keeps both the MFMA operand reads and the dequantised-W writes free of
+//    bank conflicts without padding.
+//  * Packed W, zeros and scales of stage s+2 are loaded into registers while
+//    W of stage s+1 is dequantised between the MFMAs of stage s (scheduling
+//    groups interleave a few VALU ops after each MFMA) and written to LDS
+//    n-major with k contiguous. One s_barrier per stage; waits are explicit
+//    vmcnt/lgkmcnt counts, so loads of later stages stay in flight.
+//  * f16 dequant: one v_perm_b32 gathers the byte holding the column's lane
+//    from two rows, one v_bitop3_b32 forms f16 1024 + q (low nibble) or
+//    64 + q (high nibble), then an exact v_pk_add_f16 of the zero and one
+//    v_pk_mul_f16 of the scale: the correctly rounded f16 of (q - z) * s,
+//    the reference's F = f16 value. bf16: (q - z) * s exact in f32, rounded
+//    once to bf16.
+//  * Tiles are rastered in groups of a few row tiles and remapped so each
+//    XCD runs a contiguous block of them, sharing X and W in its L2.
+//  * Skinny problems (M <= 128) split K across workgroups; partials are
+//    summed in split order by the last workgroup to arrive on its tile.
+// gemm_kernel (generic, 128x128, padded LDS, VGPR-staged loads) takes fp32
+// activations (v_mfma_f32_32x32x2_f32, W dequantised in f32 exactly as the
+// reference's F = f32 kernel) and every shape the large-tile kernel does not.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
