@@ -93,6 +93,18 @@ __device__ __forceinline__ void store_f32_any(void* p, int64_t i, int32_t t, flo
   else ((bf16_t*)p)[i] = from_f32<bf16_t>(v);
 }
 
+// Packed lane L of two words as f16x2 magic numbers: the byte holding lane L
+// of w0 and of w1 goes to the two halves (v_perm_b32), then one v_bitop3
+// keeps the nibble and ORs in the exponent: low nibble (even L) -> 0x6400 | q
+// = 1024 + q, high nibble (odd L) -> 0x5400 | q << 4 = 64 + q (mantissa unit
+// 1/16 at exponent 6). L must be a compile-time constant after inlining.
+__device__ __forceinline__ uint32_t nib_f16x2(uint32_t w0, uint32_t w1, int L) {
+  const uint32_t b = (uint32_t)L >> 1;
+  const uint32_t h = __builtin_amdgcn_perm(w1, w0, b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24));
+  return (L & 1) ? __builtin_amdgcn_bitop3_b32(h, 0x00F000F0u, 0x54005400u, 0xEA)
+                 : __builtin_amdgcn_bitop3_b32(h, 0x000F000Fu, 0x64006400u, 0xEA);
+}
+
 // Raw buffer access: a 128-bit resource (base, byte size) in SGPRs plus a
 // per-lane byte offset (VGPR) and a wave-uniform byte offset (SGPR), so a
 // strided walk over rows costs no per-load VALU address arithmetic.

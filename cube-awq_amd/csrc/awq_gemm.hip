@@ -388,18 +388,6 @@ constexpr int waitcnt_imm(int vm, int lgkm) {
 }
 __device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
 
-// Packed lane L of two words as f16x2 magic numbers: the byte holding lane L
-// of w0 and of w1 goes to the two halves (v_perm_b32), then one v_bitop3
-// keeps the nibble and ORs in the exponent: low nibble (even L) -> 0x6400 | q
-// = 1024 + q, high nibble (odd L) -> 0x5400 | q << 4 = 64 + q (mantissa unit
-// 1/16 at exponent 6). L must be a compile-time constant after inlining.
-__device__ __forceinline__ uint32_t nib_f16x2(uint32_t w0, uint32_t w1, int L) {
-  const uint32_t b = (uint32_t)L >> 1;
-  const uint32_t h = __builtin_amdgcn_perm(w1, w0, b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24));
-  return (L & 1) ? __builtin_amdgcn_bitop3_b32(h, 0x00F000F0u, 0x54005400u, 0xEA)
-                 : __builtin_amdgcn_bitop3_b32(h, 0x000F000Fu, 0x64006400u, 0xEA);
-}
-
 // 16 bytes per lane from a buffer straight into LDS: lane l's data lands at
 // dst + 16 l (dst is wave-uniform; it goes through M0).
 __device__ __forceinline__ void lds_dma16(rsrc_t r, unsigned char* dst, uint32_t voff, uint32_t soff) {

@@ -362,6 +362,287 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Small-M path on the matrix cores (2 <= rows <= 16 per launch).
+//
+// The VALU path above spends one FMA per weight per activation row, so its
+// cost grows with M. Here the weights feed v_mfma_f32_16x16x32_f16 as exact
+// f16 integers q - z (|q - z| <= 15) and each group's partial sums are scaled
+// once, so the arithmetic per weight is the same for every M <= 16:
+//   acc[m, n] = sum_k x[m, k] * (q[k, n] - z[n]);  y[m, n] += s[n] * acc[m, n]
+// Activations that are not f16 are first scaled, per activation row and
+// wave, by the power of two that puts the row's largest |x| in [2^14, 2^15)
+// (exact; undone when the scale s is applied), then split as x = hi + lo with
+// hi = f16(x), lo = f16(x - hi): |x - hi - lo| <= 2^-22 max|x|, and no f16
+// overflow or denormal loss whatever the magnitude of x. Both halves run
+// through the MFMA; products of f16 values with 4-bit integers are exact in
+// the fp32 accumulators, so the result keeps fp32 accuracy. (Non-finite
+// activations give non-finite outputs, NaN where an fp32 sum might give inf.)
+//
+// Weights are read exactly as in the VALU path (lane l owns packed word
+// chunk*64 + l, one 256-byte row segment per load), then a 4x4 transpose of
+// 16-lane groups (v_permlane32_swap, v_permlane16_swap) gives lane group b
+// rows 8b..8b+7 of 16 packs: the B operand layout of the 16x16x32 MFMA
+// (lane l supplies 8 consecutive k of column l % 16). Reading the weights in
+// that layout directly (4 rows x 64 bytes per load) measured 30 % slower.
+// One 32-row step of a wave: 32 transposes, 4 x 8 MFMA operands (packed lane
+// c of 16 packs, 1.5 VALU ops per weight: v_perm_b32, v_bitop3_b32, exact
+// v_pk_add_f16 of -(1024 + z)), 32 MFMAs (64 with the low half of x).
+// Waves of a workgroup are summed through LDS in a fixed order, K splits
+// through the workspace exactly as in the VALU path.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef h2_t f16x2;
+
+__device__ __forceinline__ void tr4(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
+  // In: r_b's 16-lane group a holds block (a, b). Out: r_a's group b holds it.
+  auto s02 = __builtin_amdgcn_permlane32_swap(r0, r2, false, false);
+  auto s13 = __builtin_amdgcn_permlane32_swap(r1, r3, false, false);
+  auto t01 = __builtin_amdgcn_permlane16_swap(s02[0], s13[0], false, false);
+  auto t23 = __builtin_amdgcn_permlane16_swap(s02[1], s13[1], false, false);
+  r0 = t01[0];
+  r1 = t01[1];
+  r2 = t23[0];
+  r3 = t23[1];
+}
+
+template <int XT>
+__device__ __forceinline__ void load_x8(const void* x, int64_t i, float (&v)[8]) {
+  if constexpr (XT == AWQ_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + i);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    using X = typename Elem<XT>::type;
+    const u32x4_t r = *reinterpret_cast<const u32x4_t*>(static_cast<const X*>(x) + i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint16_t h = (uint16_t)(r[e >> 1] >> (16 * (e & 1)));
+      v[e] = to_f32(__builtin_bit_cast(X, h));
+    }
+  }
+}
+
+template <int XT, int MV, int WAVES, int RPW>
+__global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
+  constexpr int kChunkCols = 512;
+  constexpr bool kLo = XT != AWQ_F16;
+  constexpr int kSteps = RPW / 32;
+  static_assert(RPW == 32 || RPW == 64, "rows per wave: whole 32-row MFMA steps");
+  static_assert(MV == 8, "row tile");
+  static_assert(WAVES == 4 || WAVES == 8, "waves per workgroup");
+  __shared__ float red[WAVES][MV][kChunkCols];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int chunk = blockIdx.x;
+  const int split = blockIdx.y;
+  const int np = a.N >> 3;
+  const int rows = a.rows;
+  const int lg = lane >> 4, lj = lane & 15;
+  const int pack_c = min(chunk * 64 + lane, np - 1);  // clamped: loads stay in bounds
+
+  const int k0 = (split * WAVES + wave) * RPW;  // one run inside one group
+  const bool live = k0 < a.K;
+  const int kc = live ? k0 : 0;
+  const int grp = kc / a.group;
+
+  // ---- loads: the wave's RPW weight rows first, then the zero words and
+  // scales of the 4 packs this lane feeds (pack chunk*64 + 16 s + lj), then
+  // its activations.
+  const rsrc_t wr = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
+  const uint32_t voff = (uint32_t)pack_c * 4u;
+  const uint32_t row_bytes = (uint32_t)np * 4u;
+  uint32_t w[RPW];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) w[r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + r) * row_bytes);
+  uint32_t zq[4];
+  RawScales sraw[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int pk = min(chunk * 64 + 16 * s + lj, np - 1);
+    zq[s] = a.qzeros[(int64_t)grp * np + pk];
+    sraw[s] = load_scales_raw(a.scales, a.st, (int64_t)grp * a.N + (int64_t)pk * 8);
+  }
+  // A operand: lane (lg, lj) holds x[lj, k + 8 lg .. k + 8 lg + 7] of each step.
+  const bool xrow_ok = lj < rows;
+  const int64_t xbase = (int64_t)min(lj, rows - 1) * a.K + kc + 8 * lg;
+  float xv[kSteps][8];
+#pragma unroll
+  for (int b = 0; b < kSteps; ++b) {
+    load_x8<XT>(a.x, xbase + 32 * b, xv[b]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) xv[b][e] = xrow_ok ? xv[b][e] : 0.f;
+  }
+  // Row scale (not for f16 activations, which are exact as they are): the
+  // largest |x| of row lj over this wave's rows goes to [2^14, 2^15).
+  float xdown[4] = {1.f, 1.f, 1.f, 1.f};  // undo factor of D rows 4 lg + r
+  if constexpr (kLo) {
+    float mx = 0.f;
+#pragma unroll
+    for (int b = 0; b < kSteps; ++b)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(xv[b][e]));
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    int ex;
+    (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
+    const int up = min(max(15 - ex, -126), 127);
+    const float fup = ldexpf(1.f, up);
+#pragma unroll
+    for (int b = 0; b < kSteps; ++b)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[b][e] *= fup;
+    const float down = ldexpf(1.f, -up);
+    // Row 4 lg + r of the D layout is row lj = 4 lg + r of the A layout.
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xdown[r] = __shfl(down, 4 * lg + r, 64);
+  }
+  f16x8_t ahi[kSteps], alo[kSteps];
+#pragma unroll
+  for (int b = 0; b < kSteps; ++b)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const _Float16 h = (_Float16)xv[b][e];
+      ahi[b][e] = h;
+      alo[b][e] = (_Float16)(xv[b][e] - (float)h);
+    }
+
+  // ---- transpose: w[32 b + 8 s + u] becomes, in lane group lg, row
+  // 32 b + 8 lg + u of pack chunk*64 + 16 s + lj.
+#pragma unroll
+  for (int b = 0; b < kSteps; ++b)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) tr4(w[32 * b + u], w[32 * b + 8 + u], w[32 * b + 16 + u], w[32 * b + 24 + u]);
+
+  // ---- per pack set s: MFMAs over the wave's rows, then scale and write the
+  // set's 8 x 128 partial sums to this wave's LDS slot. acc[c][r] is row
+  // 4 lg + r of packed lane c of pack chunk*64 + 16 s + lj; columns of a pack
+  // in order take packed lane kAwqLaneOfCol[j] (AutoAWQ) or j (sequential).
+  const bool seq = a.seq != 0;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    f32x4_t acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (live) {
+#pragma unroll
+      for (int b = 0; b < kSteps; ++b) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const f16x2 fz = __builtin_bit_cast(f16x2, nib_f16x2(zq[s], zq[s], c));
+          f16x8_t bq;
+#pragma unroll
+          for (int u = 0; u < 8; u += 2) {
+            const f16x2 d =
+                __builtin_bit_cast(f16x2, nib_f16x2(w[32 * b + 8 * s + u], w[32 * b + 8 * s + u + 1], c)) - fz;
+            bq[u] = d[0];
+            bq[u + 1] = d[1];
+          }
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b], bq, acc[c], 0, 0, 0);
+          if constexpr (kLo) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b], bq, acc[c], 0, 0, 0);
+        }
+      }
+    }
+    float sl[8];
+    scales_to_f32(sraw[s], a.st, sl);  // column order
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * lg + r;
+      if (m < MV) {
+        float o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float v = seq ? acc[j][r] : acc[awq_lane_of_col(j)][r];
+          o[j] = v * sl[j] * xdown[r];
+        }
+        float4* d4 = reinterpret_cast<float4*>(&red[wave][m][8 * (16 * s + lj)]);
+        d4[0] = make_float4(o[0], o[1], o[2], o[3]);
+        d4[1] = make_float4(o[4], o[5], o[6], o[7]);
+      }
+    }
+  }
+  __syncthreads();
+
+  constexpr int kOut = MV * kChunkCols;
+  constexpr int kPer = (kOut + 64 * WAVES - 1) / (64 * WAVES);
+  float res[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = threadIdx.x + i * 64 * WAVES;
+    float v = 0.f;
+    if (o < kOut) {
+      const int m = o / kChunkCols, c = o % kChunkCols;
+#pragma unroll
+      for (int ww = 0; ww < WAVES; ++ww) v += red[ww][m][c];
+    }
+    res[i] = v;
+  }
+
+  const int col_base = chunk * kChunkCols;
+  if (a.splits > 1) {
+    // Same handshake as the VALU path: agent-scope partial stores, completion
+    // wait, arrival count; the last workgroup sums the splits in order.
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int o = threadIdx.x + i * 64 * WAVES;
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      if (o < kOut && m < rows && col_base + c < a.N)
+        __hip_atomic_store(&a.partial[((int64_t)split * MV + m) * a.N + col_base + c], res[i],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCounterStride], 1u,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int o = threadIdx.x + i * 64 * WAVES;
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      if (o < kOut && m < rows && col_base + c < a.N) {
+        const float* src = a.partial + (int64_t)m * a.N + col_base + c;
+        const int64_t stride = (int64_t)MV * a.N;
+        float v = 0.f;
+        int s = 0;
+        for (; s + 8 <= a.splits; s += 8) {
+          float t8[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            t8[j] = __hip_atomic_load(src + (s + j) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) v += t8[j];
+        }
+        for (; s < a.splits; ++s)
+          v += __hip_atomic_load(src + s * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        res[i] = v;
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = threadIdx.x + i * 64 * WAVES;
+    const int m = o / kChunkCols, c = o % kChunkCols;
+    const int n = col_base + c;
+    if (o < kOut && m < rows && n < a.N) {
+      float v = res[i];
+      if (a.bias) v += load_f32_any(a.bias, n, a.bt);
+      store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, v);
+    }
+  }
+}
+
 int env_int(const char* name, int dflt) {
   const char* e = std::getenv(name);
   return e ? std::atoi(e) : dflt;
@@ -453,8 +734,69 @@ void launch_rpw(const GemmProblem& p) {
   panic("decode GEMV: no kernel configuration for this shape");
 }
 
+template <int XT, int MV, int WAVES, int RPW>
+void launch_mfma_cfg(const GemmProblem& p) {
+  const int np = (int)(p.N / 8);
+  const int chunks = (np + 63) / 64;
+  const int splits = (int)((p.K + WAVES * RPW - 1) / (WAVES * RPW));
+  GemvArgs a{};
+  a.x = p.x;
+  a.qweight = p.qweight;
+  a.qzeros = p.qzeros;
+  a.scales = p.scales;
+  a.bias = p.bias;
+  a.y = p.y;
+  a.st = p.st;
+  a.bt = p.bt;
+  a.yt = p.yt;
+  a.rows = (int32_t)p.rows;
+  a.K = (int32_t)p.K;
+  a.N = (int32_t)p.N;
+  a.group = (int32_t)p.group;
+  a.splits = splits;
+  a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  if (splits > 1) {
+    const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
+    const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
+    a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
+    a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
+  }
+  hipLaunchKernelGGL((gemv_mfma_kernel<XT, MV, WAVES, RPW>), dim3(chunks, splits), dim3(64 * WAVES),
+                     0, p.stream, a);
+  check_hip(hipGetLastError(), "gemv mfma kernel launch");
+}
+
+// Small-M matrix-core path: 8 waves per workgroup, 64 rows per wave when the
+// group allows and that still gives >= 192 workgroups, else 32. (Fewer waves
+// per workgroup measured slower at every shape tried: more K splits cost
+// more in the final reduction than the extra workgroups gain.)
+template <int XT, int MV>
+void launch_mfma(const GemmProblem& p) {
+  const int chunks = (int)((p.N / 8 + 63) / 64);
+  auto wgs = [&](int w, int r) {
+    return (int64_t)chunks * ((p.K + (int64_t)w * r - 1) / ((int64_t)w * r));
+  };
+  int rpw = p.group % 64 == 0 ? 64 : 32;
+  int waves = 8;
+  if (rpw == 64 && wgs(8, 64) < 192) rpw = 32;
+  if (int v = env_int("AWQ_MFMA_WAVES", 0); v == 4 || v == 8) waves = v;
+  if (int v = env_int("AWQ_MFMA_RPW", 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
+  if (waves == 8 && rpw == 64) return launch_mfma_cfg<XT, MV, 8, 64>(p);
+  if (waves == 8) return launch_mfma_cfg<XT, MV, 8, 32>(p);
+  if (rpw == 64) return launch_mfma_cfg<XT, MV, 4, 64>(p);
+  return launch_mfma_cfg<XT, MV, 4, 32>(p);
+}
+
 template <int XT>
 void launch_xt(const GemmProblem& p) {
+  // 2..8 rows: matrix cores, whose cost per weight does not grow with M,
+  // except 2 rows of a small matrix (<= 4096 x 4096), where the VALU kernel
+  // measured faster (AWQ_DECODE_MFMA=0/1 forces the choice).
+  const int force = env_int("AWQ_DECODE_MFMA", -1);
+  const bool small2 = p.rows == 2 && p.K * p.N <= 4096ll * 4096ll;
+  const bool mfma_ok = p.rows >= 2 && p.group % 32 == 0 && p.K % 32 == 0 &&
+                       (force == 1 || (force != 0 && !small2));
+  if (mfma_ok) return launch_mfma<XT, 8>(p);
   if (p.rows <= 1) launch_rpw<XT, 1, 16>(p);
   else if (p.rows <= 2) launch_rpw<XT, 2, 16>(p);
   else if (p.rows <= 4) launch_rpw<XT, 4, 8>(p);
