@@ -35,6 +35,7 @@
 // Algorithmic HBM bytes per call: K*N/2 (qweight) + (K/g)*(N/8)*4 (qzeros) +
 // (K/g)*N*sizeof(scale) + M*K*sizeof(x) + M*N*sizeof(y).
 #include <cstdlib>
+#include <type_traits>
 
 #include "awq_common.h"
 
@@ -523,8 +524,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   // 4 lg + r of packed lane c of pack chunk*64 + 16 s + lj; columns of a pack
   // in order take packed lane kAwqLaneOfCol[j] (AutoAWQ) or j (sequential).
   const bool seq = a.seq != 0;
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
+  // One body per pack set with s a compile-time constant: every register
+  // index below must be static (a runtime s turns w[...] into indexed moves).
+  auto pack_set = [&](auto s_const) {
+    constexpr int s = decltype(s_const)::value;
     f32x4_t acc[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -564,7 +567,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
         d4[1] = make_float4(o[4], o[5], o[6], o[7]);
       }
     }
-  }
+  };
+  pack_set(std::integral_constant<int, 0>{});
+  pack_set(std::integral_constant<int, 1>{});
+  pack_set(std::integral_constant<int, 2>{});
+  pack_set(std::integral_constant<int, 3>{});
   __syncthreads();
 
   constexpr int kOut = MV * kChunkCols;
