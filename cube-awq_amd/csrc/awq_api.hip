@@ -161,7 +161,7 @@ static void run_gemm(GemmProblem p, int64_t launch_m) {
   check_aligned(p.y, "output");
   if (p.bias) check_aligned(p.bias, "bias");
   if (p.rows <= 0 || p.N == 0) return;
-  if (launch_m <= kDecodeMThreshold) {
+  if (launch_m <= kDecodeMThreshold || small_m_mfma_ok(p, launch_m)) {
     launch_gemv(p);
   } else {
     launch_gemm(p);

@@ -173,8 +173,11 @@ struct DequantProblem {
 
 // Kernel launchers (defined in the .hip translation units).
 void launch_dequant(const DequantProblem& p);
-void launch_gemv(const GemmProblem& p);   // rows <= 8
+void launch_gemv(const GemmProblem& p);   // rows <= 8, and 9..16 when small_m_mfma_ok
 void launch_gemm(const GemmProblem& p);   // rows > 8
+// 9..16 rows run on the matrix-core decode kernel (16-row tile) when its
+// constraints hold (group % 32, K % 32); AWQ_SMALLM_MFMA=0 turns it off.
+bool small_m_mfma_ok(const GemmProblem& p, int64_t launch_m);
 
 // Per-(device, stream, slot) device workspace, grown on demand and never shrunk.
 // kWsCounters is zero-filled when (re)allocated and kernels leave it zero;

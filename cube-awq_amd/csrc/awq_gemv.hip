@@ -432,9 +432,14 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   constexpr bool kLo = XT != AWQ_F16;
   constexpr int kSteps = RPW / 32;
   static_assert(RPW == 32 || RPW == 64, "rows per wave: whole 32-row MFMA steps");
-  static_assert(MV == 8, "row tile");
+  static_assert(MV == 2 || MV == 4 || MV == 8 || MV == 16, "rows kept (the MFMA tile has 16)");
+  // LDS partial slots: one per wave for 8 rows; for 16 rows (128 KB for 4
+  // slots) waves w and w + 4 share slot w: the upper waves store, the lower
+  // ones add after a barrier (per pack set, so the compute stays parallel).
+  constexpr int kSlots = MV == 16 ? WAVES / 2 : WAVES;
+  constexpr bool kTwoRounds = kSlots < WAVES;
   static_assert(WAVES == 4 || WAVES == 8, "waves per workgroup");
-  __shared__ float red[WAVES][MV][kChunkCols];
+  __shared__ float red[kSlots][MV][kChunkCols];
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
@@ -444,6 +449,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   const int np = a.N >> 3;
   const int rows = a.rows;
   const int lg = lane >> 4, lj = lane & 15;
+  const int slot = wave % kSlots;
   const int pack_c = min(chunk * 64 + lane, np - 1);  // clamped: loads stay in bounds
 
   const int k0 = (split * WAVES + wave) * RPW;  // one run inside one group
@@ -552,20 +558,38 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
     }
     float sl[8];
     scales_to_f32(sraw[s], a.st, sl);  // column order
+    float o[4][8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * lg + r;
-      if (m < MV) {
-        float o[8];
+    for (int r = 0; r < 4; ++r)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = seq ? acc[j][r] : acc[awq_lane_of_col(j)][r];
-          o[j] = v * sl[j] * xdown[r];
-        }
-        float4* d4 = reinterpret_cast<float4*>(&red[wave][m][8 * (16 * s + lj)]);
-        d4[0] = make_float4(o[0], o[1], o[2], o[3]);
-        d4[1] = make_float4(o[4], o[5], o[6], o[7]);
+      for (int j = 0; j < 8; ++j) {
+        const float v = seq ? acc[j][r] : acc[awq_lane_of_col(j)][r];
+        o[r][j] = v * sl[j] * xdown[r];
       }
+    auto store = [&](bool add) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * lg + r;
+        if (m < MV) {
+          float4* d4 = reinterpret_cast<float4*>(&red[slot][m][8 * (16 * s + lj)]);
+          float4 v0 = make_float4(o[r][0], o[r][1], o[r][2], o[r][3]);
+          float4 v1 = make_float4(o[r][4], o[r][5], o[r][6], o[r][7]);
+          if (add) {
+            const float4 p0 = d4[0], p1 = d4[1];
+            v0 = make_float4(v0.x + p0.x, v0.y + p0.y, v0.z + p0.z, v0.w + p0.w);
+            v1 = make_float4(v1.x + p1.x, v1.y + p1.y, v1.z + p1.z, v1.w + p1.w);
+          }
+          d4[0] = v0;
+          d4[1] = v1;
+        }
+      }
+    };
+    if constexpr (kTwoRounds) {
+      if (wave >= kSlots) store(false);
+      __syncthreads();
+      if (wave < kSlots) store(true);
+    } else {
+      store(false);
     }
   };
   pack_set(std::integral_constant<int, 0>{});
@@ -584,7 +608,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
     if (o < kOut) {
       const int m = o / kChunkCols, c = o % kChunkCols;
 #pragma unroll
-      for (int ww = 0; ww < WAVES; ++ww) v += red[ww][m][c];
+      for (int ww = 0; ww < kSlots; ++ww) v += red[ww][m][c];
     }
     res[i] = v;
   }
@@ -610,27 +634,37 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
+    // Each thread's kPer outputs, kSB splits at a time: kPer * kSB loads in
+    // flight (one output after another would leave one CU latency-bound on
+    // splits x rows x 2 KB); every output still sums its splits in order.
+    constexpr int kSB = kPer >= 16 ? 4 : 8;
+    const int64_t stride = (int64_t)MV * a.N;
+    const float* src[kPer];
+    bool ok[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int o = threadIdx.x + i * 64 * WAVES;
       const int m = o / kChunkCols, c = o % kChunkCols;
-      if (o < kOut && m < rows && col_base + c < a.N) {
-        const float* src = a.partial + (int64_t)m * a.N + col_base + c;
-        const int64_t stride = (int64_t)MV * a.N;
-        float v = 0.f;
-        int s = 0;
-        for (; s + 8 <= a.splits; s += 8) {
-          float t8[8];
+      ok[i] = o < kOut && m < rows && col_base + c < a.N;
+      // Rows past M read row M-1's partials (cached, discarded): unconditional
+      // loads keep the batch in flight.
+      src[i] = a.partial + (int64_t)min(m, rows - 1) * a.N + min(col_base + c, a.N - 1);
+      res[i] = 0.f;
+    }
+    for (int s0 = 0; s0 < a.splits; s0 += kSB) {
+      float t[kPer][kSB];
 #pragma unroll
-          for (int j = 0; j < 8; ++j)
-            t8[j] = __hip_atomic_load(src + (s + j) * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int i = 0; i < kPer; ++i)
 #pragma unroll
-          for (int j = 0; j < 8; ++j) v += t8[j];
+        for (int j = 0; j < kSB; ++j) {
+          const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
+          t[i][j] = __hip_atomic_load(src[i] + sj * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        for (; s < a.splits; ++s)
-          v += __hip_atomic_load(src + s * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        res[i] = v;
-      }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+#pragma unroll
+        for (int j = 0; j < kSB; ++j)
+          if (s0 + j < a.splits) res[i] += t[i][j];
     }
     if (threadIdx.x == 0)
       __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
@@ -797,13 +831,21 @@ void launch_mfma(const GemmProblem& p) {
 template <int XT>
 void launch_xt(const GemmProblem& p) {
   // 2..8 rows: matrix cores, whose cost per weight does not grow with M,
-  // except 2 rows of a small matrix (<= 4096 x 4096), where the VALU kernel
-  // measured faster (AWQ_DECODE_MFMA=0/1 forces the choice).
+  // except 2 rows of a small, wide matrix (K x N <= 4096 x 4096, N >= 4096),
+  // where the VALU kernel measured faster (AWQ_DECODE_MFMA=0/1 forces the
+  // choice).
   const int force = env_int("AWQ_DECODE_MFMA", -1);
-  const bool small2 = p.rows == 2 && p.K * p.N <= 4096ll * 4096ll;
+  const bool small2 = p.rows == 2 && p.K * p.N <= 4096ll * 4096ll && p.N >= 4096;
   const bool mfma_ok = p.rows >= 2 && p.group % 32 == 0 && p.K % 32 == 0 &&
                        (force == 1 || (force != 0 && !small2));
-  if (mfma_ok) return launch_mfma<XT, 8>(p);
+  if (p.rows > 8) return launch_mfma<XT, 16>(p);  // accepted by small_m_mfma_ok
+  if (mfma_ok) {
+    // Rows kept in LDS, the workspace and the final reduction (the MFMA
+    // tile always computes 16).
+    if (p.rows <= 2) return launch_mfma<XT, 2>(p);
+    if (p.rows <= 4) return launch_mfma<XT, 4>(p);
+    return launch_mfma<XT, 8>(p);
+  }
   if (p.rows <= 1) launch_rpw<XT, 1, 16>(p);
   else if (p.rows <= 2) launch_rpw<XT, 2, 16>(p);
   else if (p.rows <= 4) launch_rpw<XT, 4, 8>(p);
@@ -811,6 +853,11 @@ void launch_xt(const GemmProblem& p) {
 }
 
 }  // namespace
+
+bool small_m_mfma_ok(const GemmProblem& p, int64_t launch_m) {
+  return launch_m > 8 && launch_m <= 16 && p.rows <= 16 && p.group % 32 == 0 && p.K % 32 == 0 &&
+         env_int("AWQ_SMALLM_MFMA", 1) != 0;
+}
 
 void launch_gemv(const GemmProblem& p) {
   AWQ_ASSERT(p.K < (1ll << 31) && p.N < (1ll << 31) && p.K * (p.N / 8) < (1ll << 30),

@@ -378,3 +378,27 @@ def test_decode_mfma_activation_magnitudes(dev, row_scales):
     for m in range(M):
         assert np.isfinite(y[m]).all()
         assert oracle.rel_l2(y[m], ref[m]) <= TOL_FP32, (m, row_scales[m])
+
+
+# 9..16 rows run on the matrix-core decode kernel's 16-row tile (two-round
+# LDS reduction); AWQ_SMALLM_MFMA=0 sends them to the prefill kernels.
+@pytest.mark.parametrize("path", ["1", "0"])
+@pytest.mark.parametrize("M", [9, 12, 16])
+@pytest.mark.parametrize("x_dt", ["f32", "f16", "bf16"])
+def test_small_m_both_paths(dev, monkeypatch, path, M, x_dt):
+    monkeypatch.setenv("AWQ_SMALLM_MFMA", path)
+    K, N, g = 2048, 2080, 64
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32")
+    ref = _ref64(x, qw, qz, sc, b, g, x_dt, "f16")
+    tol = TOL_FP32 if (path == "1" or x_dt == "f32") else TOL_MFMA
+    assert oracle.rel_l2(to_host(y), ref) <= tol
+
+
+@pytest.mark.parametrize("rpw", [32, 64])
+def test_small_m_every_configuration(dev, monkeypatch, rpw):
+    monkeypatch.setenv("AWQ_MFMA_RPW", str(rpw))
+    M, K, N, g = 16, 4096, 1536, 128
+    x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f32", s_dt="f32")
+    y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f32", "f32", "f32")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, None, g, "f32", "f32")) <= TOL_FP32
