@@ -91,6 +91,44 @@ def load_awq_gemm_linear(source, prefix, device=None, scale_dtype=None):
     )
 
 
+def load_fused_awq_gemm_linear(source, prefixes, device=None, scale_dtype=None):
+    """One `AWQGEMMLinear` computing several projections of the same input in
+    one launch (e.g. q/k/v or gate/up), by concatenating their tensors along
+    N: qweight/qzeros [.., N_i/8] and scales/bias [.., N_i] side by side. Packs
+    never straddle projections (each N_i % 32 == 0), so column block i of the
+    fused output is exactly projection i. All projections must share K and the
+    group size; a bias, if any projection has one, is zero for the others.
+    Returns (layer, sizes) with sizes the N_i in order:
+    `torch.split(layer.forward(x), sizes, dim=-1)` gives the projections."""
+    parts = []
+    for prefix in prefixes:
+        qweight = _read(source, f"{prefix}.qweight")
+        qzeros = _read(source, f"{prefix}.qzeros")
+        scales = _read(source, f"{prefix}.scales")
+        k, n, group = _check_awq(qweight, qzeros, scales, need_gemm_constraints=True)
+        bias = _read(source, f"{prefix}.bias") if _has(source, f"{prefix}.bias") else None
+        if bias is not None and tuple(bias.shape) != (n,):
+            raise Panic(f"bias must be [{n}], got {list(bias.shape)}")
+        parts.append((prefix, qweight, qzeros, scales, bias, k, n, group))
+    if not parts:
+        raise Panic("no projections to fuse")
+    k0, g0 = parts[0][5], parts[0][7]
+    for prefix, _, _, _, _, k, _, group in parts:
+        if k != k0 or group != g0:
+            raise Panic(f"fused projections must share d_input and group_size: {prefix} has "
+                        f"({k}, {group}), {parts[0][0]} has ({k0}, {g0})")
+    sd = scale_dtype or parts[0][3].dtype
+    qweight = torch.cat([p[1].view(torch.int32) if p[1].dtype != torch.int32 else p[1] for p in parts], dim=1)
+    qzeros = torch.cat([p[2].view(torch.int32) if p[2].dtype != torch.int32 else p[2] for p in parts], dim=1)
+    scales = torch.cat([p[3].to(sd) for p in parts], dim=1)
+    bias = None
+    if any(p[4] is not None for p in parts):
+        bias = torch.cat([p[4].to(sd) if p[4] is not None else torch.zeros(p[6], dtype=sd) for p in parts])
+    layer = AWQGEMMLinear(qweight.contiguous().to(device), qzeros.contiguous().to(device),
+                          scales.contiguous().to(device), None if bias is None else bias.contiguous().to(device))
+    return layer, [p[6] for p in parts]
+
+
 def load_awq_linear(source, prefix, device=None, scale_dtype=None):
     """`AWQLinear` (dequantize path, sequential nibble order) from the same
     tensor names; the module's own build checks apply (N % 8, K % g, N % 32,

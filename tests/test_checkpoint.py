@@ -67,3 +67,44 @@ def test_gemm_constraints_apply():
     sc = torch.ones((3, 32), dtype=torch.float16)
     with pytest.raises(Panic, match="INNER_K"):
         checkpoint.load_awq_gemm_linear({"l.qweight": qw, "l.qzeros": qz, "l.scales": sc}, "l")
+
+
+def _proj(prefix, k, n, g, seed, bias):
+    qw = torch.from_numpy(synth.packed_nibbles(seed, k, n // 8).view(np.int32).copy())
+    qz = torch.from_numpy(synth.packed_nibbles(seed + 1, k // g, n // 8).view(np.int32).copy())
+    sc = torch.from_numpy(synth.uniform(seed + 2, (k // g, n), 0.002, 0.02, np.float16))
+    d = {f"{prefix}.qweight": qw, f"{prefix}.qzeros": qz, f"{prefix}.scales": sc}
+    if bias:
+        d[f"{prefix}.bias"] = torch.from_numpy(synth.uniform(seed + 3, (n,), -1.0, 1.0, np.float16))
+    return d
+
+
+def test_fused_projections_concatenate_along_n():
+    a = "model.layers.0.self_attn"
+    d = {}
+    d.update(_proj(f"{a}.q_proj", 256, 256, 64, 10, bias=True))
+    d.update(_proj(f"{a}.k_proj", 256, 64, 64, 20, bias=False))
+    d.update(_proj(f"{a}.v_proj", 256, 96, 64, 30, bias=True))
+    layer, sizes = checkpoint.load_fused_awq_gemm_linear(d, [f"{a}.q_proj", f"{a}.k_proj", f"{a}.v_proj"])
+    assert sizes == [256, 64, 96] and layer.group_size() == 64
+    assert tuple(layer.qweight.shape) == (256, 52) and tuple(layer.scales.shape) == (4, 416)
+    col = 0
+    for name, n in zip(("q_proj", "k_proj", "v_proj"), sizes):
+        p = f"{a}.{name}"
+        assert torch.equal(layer.qweight[:, col // 8:(col + n) // 8], d[f"{p}.qweight"])
+        assert torch.equal(layer.qzeros[:, col // 8:(col + n) // 8], d[f"{p}.qzeros"])
+        assert torch.equal(layer.scales[:, col:col + n], d[f"{p}.scales"])
+        want_b = d.get(f"{p}.bias", torch.zeros(n, dtype=torch.float16))
+        assert torch.equal(layer.bias[col:col + n], want_b)
+        col += n
+
+
+def test_fused_projections_reject_mismatched_k_or_group():
+    d = {}
+    d.update(_proj("p0", 256, 64, 64, 10, bias=False))
+    d.update(_proj("p1", 256, 64, 128, 20, bias=False))
+    with pytest.raises(Panic, match="share d_input and group_size"):
+        checkpoint.load_fused_awq_gemm_linear(d, ["p0", "p1"])
+    d.update(_proj("p2", 128, 64, 64, 30, bias=False))
+    with pytest.raises(Panic, match="share d_input and group_size"):
+        checkpoint.load_fused_awq_gemm_linear(d, ["p0", "p2"])

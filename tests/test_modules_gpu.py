@@ -93,3 +93,30 @@ def test_checkpoint_loaded_layer_forward(dev, tmp_path, M):
                           sc.astype(np.float16).astype(np.float32), g,
                           bias=b.astype(np.float16).astype(np.float32))
     assert oracle.rel_l2(y.float().cpu().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("M", [1, 4, 12, 300])
+def test_fused_qkv_projection_forward(dev, M):
+    """q/k/v fused along N (one launch) against each projection's oracle."""
+    from cube_awq import checkpoint, synth
+    K, g = 1024, 128
+    sizes = [1024, 256, 256]
+    tensors, parts = {}, []
+    for i, n in enumerate(sizes):
+        qw = synth.packed_nibbles(40 + 4 * i, K, n // 8)
+        qz = synth.packed_nibbles(41 + 4 * i, K // g, n // 8)
+        sc = synth.uniform(42 + 4 * i, (K // g, n), 0.002, 0.02, np.float16)
+        tensors[f"p{i}.qweight"] = torch.from_numpy(pack.as_int32(qw))
+        tensors[f"p{i}.qzeros"] = torch.from_numpy(pack.as_int32(qz))
+        tensors[f"p{i}.scales"] = torch.from_numpy(sc)
+        parts.append((qw, qz, sc))
+    lay, got_sizes = checkpoint.load_fused_awq_gemm_linear(tensors, ["p0", "p1", "p2"], device=dev)
+    assert got_sizes == sizes
+    x = synth.normal(synth.TID_X, (M, K), np.float16)
+    y = lay.forward(torch.from_numpy(x).to(dev))
+    torch.cuda.synchronize()
+    outs = torch.split(y.float().cpu(), sizes, dim=-1)
+    tol = 1e-3 if M <= 16 else 2e-3  # f16 output
+    for (qw, qz, sc), out in zip(parts, outs):
+        ref = oracle.gemm_f64(x.astype(np.float32), qw, qz, sc.astype(np.float32), g)
+        assert oracle.rel_l2(out.numpy(), ref) <= tol
