@@ -6,9 +6,12 @@ Headline (`value`): decode dequant-GEMV at M=1 on the Llama-3-8B gate/up shape
 U[0.002, 0.02], uniform 4-bit weights/zeros in AutoAWQ packing, f32 output),
 in GB/s of algorithmic HBM bytes per call:
     K*N/2 + (K/g)*(N/8)*4 + (K/g)*N*2 + M*K*4 + M*N*4  = 30,580,736 B.
-Secondary objects in the same JSON line: prefill at M=2048 on the same shape
-(fp16 activations, fp16 MFMA, fp32 accumulation; TFLOP/s of 2*M*N*K) and the
-standalone dequantize of K=14336, N=4096, g64 (f32 out; GB/s of read+write).
+Secondary objects in the same JSON line: the decode at M=4 and 8 and a
+measured read-stream ceiling (a plain streaming-read kernel from the bench
+helper library over buffers of the decode call's size); prefill at M=2048 on
+the same shape (fp16 activations, fp16 MFMA, fp32 accumulation; TFLOP/s of
+2*M*N*K), with M=16, 64, 512 beside it; the standalone dequantize of K=14336,
+N=4096, g64 (f32 out; GB/s of read+write).
 
 Method: inputs resident in HBM before timing; the decode rotates over
 ceil(512 MB / bytes-per-call) independent weight copies so the 256 MB MALL
@@ -144,6 +147,44 @@ def main():
         ms, calls, wall = graph_time(dec, 100, args.warmup, args.steps)
         gbs = dec_bytes / (ms * 1e-3) / 1e9
         out["decode"] = dict(ms=ms, calls=calls, wall_s=wall, gbs=gbs, bytes=dec_bytes, copies=copies)
+
+        if args.only is None:
+            # The other decode rows of the same shape (matrix-core kernel).
+            out["decode_rows"] = {}
+            for mr in (4, 8):
+                xr = torch.from_numpy(synth.normal(synth.TID_X, (mr, K), np.float32)).to(dev)
+                yr = torch.empty((mr, N), dtype=torch.float32, device=dev)
+                r_bytes = dec_bytes + (mr - 1) * (K + N) * 4
+
+                def dec_r(i, xr=xr, yr=yr, mr=mr):
+                    w = ws[i % copies]
+                    call_gemm(xr, _lib.AWQ_F32, w[0], w[1], w[2], _lib.AWQ_F16, yr, _lib.AWQ_F32, mr, K, N, G)
+
+                rms, _, _ = graph_time(dec_r, 100, 50, 2000)
+                out["decode_rows"][mr] = dict(us=rms * 1e3, gbs=r_bytes / (rms * 1e-3) / 1e9)
+
+            # Measured read-stream ceiling: a plain streaming-read kernel (the
+            # bench helper library, not the AWQ library) over buffers of the
+            # decode call's size, rotated the same way, timed the same way.
+            import ctypes
+            hl = ctypes.CDLL(os.path.join(REPO, "cube-awq_amd", "lib", "libawq_bench_gfx950.so"))
+            hl.awqbench_read_stream.restype = ctypes.c_int
+            hl.awqbench_read_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                                ctypes.c_int, ctypes.c_void_p]
+            rs_bytes = dec_bytes // 16 * 16
+            bufs = [torch.ones(rs_bytes // 4, dtype=torch.float32, device=dev) for _ in range(copies)]
+            grid = 2048
+            sink = torch.zeros(grid, dtype=torch.int32, device=dev)
+
+            def stream(i):
+                rc = hl.awqbench_read_stream(bufs[i % copies].data_ptr(), rs_bytes, sink.data_ptr(),
+                                             grid, cur_stream())
+                if rc:
+                    raise RuntimeError(f"read-stream launch failed: {rc}")
+
+            sms, _, _ = graph_time(stream, 100, 50, 2000)
+            out["read_stream"] = dict(us=sms * 1e3, gbs=rs_bytes / (sms * 1e-3) / 1e9)
+            del bufs
         del ws
 
     # ---------------- prefill M=2048, 4096 -> 14336 ---------------------------------------
@@ -163,6 +204,17 @@ def main():
         ms, calls, wall = graph_time(pre, 10, 5, steps)
         out["prefill"] = dict(ms=ms, calls=calls, wall_s=wall, tflops=pf_flops / (ms * 1e-3) / 1e12)
         if args.only is None:
+            # The other prefill rows of the same shape.
+            out["prefill_rows"] = {}
+            for mr in (16, 64, 512):
+                xr = xp[:mr].contiguous()
+                yr = torch.empty((mr, N), dtype=torch.float16, device=dev)
+
+                def pre_r(i, xr=xr, yr=yr, mr=mr):
+                    call_gemm(xr, _lib.AWQ_F16, qw, qz, sc, _lib.AWQ_F16, yr, _lib.AWQ_F16, mr, K, N, G)
+
+                rms, _, _ = graph_time(pre_r, 20, 10, 200)
+                out["prefill_rows"][mr] = dict(us=rms * 1e3, tflops=2.0 * mr * N * K / (rms * 1e-3) / 1e12)
             # Context, not a roofline: the library dense fp16 GEMM (torch ->
             # hipBLASLt) of the same shape on unquantised f16 weights, W given
             # as [N, K] (its faster layout). The fused kernel additionally
@@ -263,6 +315,14 @@ def main():
                            "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
                            "traffic": tr, "algorithmic_bytes": dec_bytes,
                            "rotating_copies": d["copies"], "us_per_call": round(d["ms"] * 1e3, 3)}
+        if "read_stream" in out:
+            r = out["read_stream"]
+            res["roofline"]["measured_read_stream_gbs"] = round(r["gbs"], 1)
+            res["roofline"]["frac_of_read_stream"] = round(d["gbs"] / r["gbs"], 4)
+        if "decode_rows" in out:
+            res["decode_rows_4096x14336"] = {
+                f"M={m}": {"us_per_call": round(v["us"], 3), "gbs": round(v["gbs"], 1)}
+                for m, v in out["decode_rows"].items()}
     if cpu:
         res["cpu_baseline"] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in cpu.items()}
     if "prefill" in out:
@@ -275,6 +335,10 @@ def main():
                                 "dtype": "f16 in, fp32 accumulate, f16 out", "calls": p["calls"]}
         if "dense_tflops" in p:
             res["prefill_m2048"]["dense_fp16_library_gemm_tflops"] = round(p["dense_tflops"], 2)
+    if "prefill_rows" in out:
+        res["prefill_rows_4096x14336"] = {
+            f"M={m}": {"us_per_call": round(v["us"], 2), "tflops": round(v["tflops"], 1)}
+            for m, v in out["prefill_rows"].items()}
     if "dequant" in out:
         q = out["dequant"]
         res["dequant_k14336_n4096_g64"] = {
