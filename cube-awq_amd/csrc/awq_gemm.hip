@@ -1034,6 +1034,7 @@ void launch_gemm(const GemmProblem& p) {
              "prefill GEMM: tensor too large");
   const int64_t tiles = ((p.rows + 127) / 128) * ((p.N + 127) / 128);
   AWQ_ASSERT(tiles < (1ll << 31), "prefill GEMM: too many tiles");
+  if (skinny_ok(p)) return launch_skinny(p);
   switch (p.xt) {
     case AWQ_F16: launch_st<MODE_F16>(p); break;
     case AWQ_BF16: launch_st<MODE_BF16>(p); break;

@@ -1,0 +1,453 @@
+// awq_skinny.hip -- fused AWQ dequant-GEMM for skinny problems (17..128 rows,
+// f16 activations) on gfx950.
+//
+// Y[M, N] = X[M, K] . W[K, N], W[k, n] = f16((q - z) * s), the reference's
+// F = f16 dequantised weight (gemm_awq, src/kernel/awq_kernel_gemm.rs:181-439),
+// accumulated in fp32 on v_mfma_f32_16x16x32_f16.
+//
+// With few activation rows the large-tile kernel (awq_gemm.hip) is latency
+// bound: every 64-row stage of a 128..256-column tile is a load, dequantise,
+// barrier, MFMA round trip, and split-K partials of M x N floats cost as much
+// traffic as the weights. Here the weights stream as in the decode kernels:
+//  * A workgroup owns 256 columns (32 packed words = 128 bytes of each row)
+//    and a run of K; 32-row steps of W, the matching 32 columns of X and,
+//    up front, the zeros and scales of the run's groups go global -> LDS
+//    directly (buffer_load ... lds, 4 bytes per lane) into a ring of kRing
+//    steps, kRing - 1 steps ahead, with explicit vmcnt waits and one
+//    s_barrier per step.
+//  * 8 waves: wave w takes packs 8 (w & 3) .. 8 (w & 3) + 7 (64 columns, four
+//    16-column MFMA tiles) for row tiles of 16 in half (w >> 2) of the rows.
+//    Lane (lg = lane / 16, lj = lane % 16) reads the 8 words of rows
+//    8 lg .. 8 lg + 7 of pack 8 (w & 3) + (lj & 7) from LDS and builds the
+//    B operand of tile t from packed lane c = 2 t + (lj >> 3): one v_perm_b32
+//    gathers byte t of two rows, one v_bitop3_b32 makes the f16 magic 1024 + q
+//    (64 + q for the high nibble), then an exact v_pk_add_f16 of -(1024 + z)
+//    and one v_pk_mul_f16 by s: 2 VALU ops per weight.
+//  * Waves never share output rows, so there is no cross-wave reduction; K
+//    splits (grid.y) publish fp32 partials and the last workgroup to arrive on
+//    a chunk sums them in split order (deterministic), adds the bias and
+//    writes Y.
+// Algorithmic HBM bytes per call: K*N/2 + (K/g)*(N/8)*4 + (K/g)*N*sizeof(s) +
+// M*K*2 + M*N*sizeof(y).
+#include <algorithm>
+#include <cstdlib>
+
+#include "awq_common.h"
+
+namespace cube_awq {
+namespace {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kCols = 256;          // columns per workgroup (chunk)
+constexpr int kPacks = kCols / 8;   // packed words per row of a chunk
+constexpr int kStep = 32;           // K rows per step (one MFMA k-block)
+constexpr int kRing = 8;            // steps held in LDS
+constexpr int kWBlock = 8 * 128 + 32;  // eight 128-byte W rows + pad (bank spread)
+constexpr int kWSlot = (kStep / 8) * kWBlock;
+constexpr int kMaxGroups = 36;      // groups a workgroup's K run may touch
+constexpr int kCtrStride = 64;      // u32 words between arrival counters
+
+struct SkinnyArgs {
+  const void* x;
+  const uint32_t* qweight;
+  const uint32_t* qzeros;
+  const void* scales;
+  const void* bias;
+  void* y;
+  float* partial;      // [splits][M][N] when splits > 1
+  uint32_t* counters;  // one per chunk, kCtrStride apart, zero between calls
+  int32_t st, bt, yt;
+  int32_t M, K, N, group;
+  int32_t splits, steps_per_split;
+  int32_t seq;         // sequential nibble order
+};
+
+constexpr int waitcnt_vm(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
+__device__ __forceinline__ void dma4(rsrc_t r, unsigned char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, soff, 0, 0);
+}
+// 16 bytes per lane: lane l's data lands at dst + 16 l.
+__device__ __forceinline__ void dma16(rsrc_t r, unsigned char* dst, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, soff, 0, 0);
+}
+
+// Granule swizzle of an X row in LDS (64 bytes = four 16-byte granules):
+// granule g of row r sits in slot g ^ xswz(r), so the 16 rows one A-operand
+// read touches spread over all banks.
+__device__ __forceinline__ int xswz(int r) { return (r >> 2) & 3; }
+
+template <int MT>
+__global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
+  constexpr int kMH = MT / 2;                  // row tiles per wave
+  constexpr int kXRows = 16 * MT;
+  constexpr int kXSlot = kXRows * 64;          // 32 f16 columns of X per row
+  // 16-byte DMAs per step: W rows 8 i .. 8 i + 7 by wave i (i < 4); X rows
+  // 16 j .. 16 j + 15 by wave 4 + j % 4 (MT of them).
+  constexpr int kXPerWave = MT >= 4 ? MT / 4 : 1;
+  static_assert(MT % 2 == 0 && MT <= 8, "row tiles");
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* wring = smem;                               // kRing W slots
+  unsigned char* xring = smem + kRing * kWSlot;              // kRing X slots
+  uint32_t* zlds = reinterpret_cast<uint32_t*>(xring + kRing * kXSlot);  // [groups][32] zero words
+  unsigned char* slds = reinterpret_cast<unsigned char*>(zlds + kMaxGroups * kPacks);  // [groups][256] scales
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lg = lane >> 4, lj = lane & 15;
+  const int cg = wave & 3, mh = wave >> 2;
+  const int chunk = blockIdx.x, split = blockIdx.y;
+  const int np = a.N >> 3;
+  const int s0 = split * a.steps_per_split;
+  const int steps = min(a.steps_per_split, a.K / kStep - s0);
+  const int k_begin = s0 * kStep;
+  const int g_first = k_begin / a.group;
+  const int es = a.st == AWQ_F32 ? 4 : 2;
+
+  // ---- prologue DMAs: zeros and scales of the run's groups (wave 0 and 1),
+  // then the first kRing - 1 steps of W and X (every wave) ---------------------
+  const int ngroups = (k_begin + steps * kStep - 1) / a.group - g_first + 1;
+  const rsrc_t zres = make_rsrc(a.qzeros, (uint32_t)((a.K / a.group) * np * 4));
+  const rsrc_t sres = make_rsrc(a.scales, (uint32_t)((int64_t)(a.K / a.group) * a.N * es));
+  if (wave == 0) {
+    // lane l: zero word of pack (l & 31) of group 2 i + (l >> 5)
+    for (int gi = 0; gi < ngroups; gi += 2) {
+      const int gr = gi + (lane >> 5);
+      const int pk = min(chunk * kPacks + (lane & 31), np - 1);
+      const int grc = min(g_first + gr, a.K / a.group - 1);
+      dma4(zres, reinterpret_cast<unsigned char*>(zlds + gi * kPacks), (uint32_t)(grc * np + pk) * 4u, 0);
+    }
+  } else if (wave == 1) {
+    // scales of the chunk's 256 columns per group: 512 (f16) or 1024 (f32) bytes
+    const int row_bytes = kCols * es;
+    for (int gi = 0; gi < ngroups; ++gi) {
+      const int grc = min(g_first + gi, a.K / a.group - 1);
+      for (int o = 0; o < row_bytes; o += 256) {
+        const int col_byte = min(chunk * kCols * es + o + lane * 4, a.N * es - 4);
+        dma4(sres, slds + gi * kCols * 4 + o, (uint32_t)((int64_t)grc * a.N * es + col_byte), 0);
+      }
+    }
+  }
+
+  const rsrc_t wres = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
+  const rsrc_t xres = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
+  const uint32_t row_bytes_w = (uint32_t)np * 4u;
+  // W (waves 0..3): wave i moves rows 8 i .. 8 i + 7 of a step; lane l -> row
+  // 8 i + (l >> 3), packs 4 (l & 7) .. + 3 (16 bytes; clamped at the last pack).
+  const uint32_t wvoff = (uint32_t)(lane >> 3) * row_bytes_w +
+                         (uint32_t)min(chunk * kPacks + 4 * (lane & 7), np - 4) * 4u;
+  // X (waves 4..7): rows 16 j .. 16 j + 15; lane l -> row + (l >> 2), slot l & 3
+  // holding granule (l & 3) ^ xswz(row) (16 bytes = 8 f16 columns).
+  const int xw = wave - 4;
+  const int n_xins = xw < 0 ? 0 : (MT >= 4 ? kXPerWave : (xw < MT ? 1 : 0));
+  uint32_t xvoff[kXPerWave];
+#pragma unroll
+  for (int i = 0; i < kXPerWave; ++i) {
+    const int j = (xw < 0 ? 0 : xw) + 4 * i;
+    const int r = 16 * j + (lane >> 2);
+    const int g = (lane & 3) ^ xswz(r);
+    const int rc = min(r, a.M - 1);  // rows past M read row M - 1 (never stored)
+    xvoff[i] = (uint32_t)(((int64_t)rc * a.K) * 2 + g * 16);
+  }
+  auto issue = [&](int s) {
+    const int slot = s % kRing;
+    const uint32_t k = (uint32_t)((s0 + s) * kStep);
+    if (wave < 4) {
+      dma16(wres, wring + slot * kWSlot + wave * kWBlock, wvoff, (k + 8 * wave) * row_bytes_w);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kXPerWave; ++i)
+        if (i < n_xins) dma16(xres, xring + slot * kXSlot + (xw + 4 * i) * 1024, xvoff[i], k * 2u);
+    }
+  };
+  // VMEM instructions this wave issues per step (uniform per wave).
+  const int per_step = wave < 4 ? 1 : n_xins;
+  const int pre = min(kRing - 2, steps);
+  for (int s = 0; s < pre; ++s) issue(s);
+
+  // ---- per-lane constants -----------------------------------------------------
+  const int pl = 8 * cg + (lj & 7);  // pack within the chunk
+  const int hh = lj >> 3;            // nibble: packed lane c = 2 t + hh
+  const bool seq = a.seq != 0;
+  // column within the pack of packed lane c = 2 t + hh
+  int colt[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int c = 2 * t + hh;
+    colt[t] = seq ? c : awq_col_of_lane(c);
+  }
+  const uint32_t hmask = hh ? 0x00F000F0u : 0x000F000Fu;
+  const uint32_t hexp = hh ? 0x54005400u : 0x64006400u;
+
+  f32x4_t acc[kMH][4];
+#pragma unroll
+  for (int i = 0; i < kMH; ++i)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  f16x2_t fz[4], fs[4];
+  int cur_g = -1;
+
+  // One step: the zero points and scales when the group changes, then the
+  // 8 W words and the A operands from LDS, 4 B operands, 4 kMH MFMAs.
+  auto compute = [&](int s) {
+    const int k = (s0 + s) * kStep;
+    const int g = k / a.group - g_first;
+    if (g != cur_g) {
+      cur_g = g;
+      const uint32_t zw = zlds[g * kPacks + pl];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const uint32_t sel = (uint32_t)t | (0x0Cu << 8) | ((4u + t) << 16) | (0x0Cu << 24);
+        const uint32_t zh = __builtin_amdgcn_perm(zw, zw, sel);
+        fz[t] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(zh, hmask, hexp, 0xEA));
+        const int col = 8 * pl + colt[t];
+        float sv;
+        if (es == 4) sv = reinterpret_cast<const float*>(slds + g * kCols * 4)[col];
+        else if (a.st == AWQ_F16) sv = (float)reinterpret_cast<const f16_t*>(slds + g * kCols * 4)[col];
+        else sv = to_f32(reinterpret_cast<const bf16_t*>(slds + g * kCols * 4)[col]);
+        const _Float16 sh = (_Float16)sv;
+        fs[t] = f16x2_t{sh, sh};
+      }
+    }
+
+    const unsigned char* wsl = wring + (s % kRing) * kWSlot;
+    uint32_t wv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int r = 8 * lg + u;
+      wv[u] = *reinterpret_cast<const uint32_t*>(wsl + (r >> 3) * kWBlock + (r & 7) * 128 + pl * 4);
+    }
+    const unsigned char* xsl = xring + (s % kRing) * kXSlot;
+    f16x8_t av[kMH];
+#pragma unroll
+    for (int i = 0; i < kMH; ++i) {
+      const int r = 16 * (mh * kMH + i) + lj;
+      av[i] = *reinterpret_cast<const f16x8_t*>(xsl + r * 64 + ((lg ^ xswz(r)) << 4));
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const uint32_t sel = (uint32_t)t | (0x0Cu << 8) | ((4u + t) << 16) | (0x0Cu << 24);
+      f16x8_t bq;
+#pragma unroll
+      for (int u = 0; u < 8; u += 2) {
+        const uint32_t h = __builtin_amdgcn_perm(wv[u + 1], wv[u], sel);
+        const f16x2_t v = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(h, hmask, hexp, 0xEA));
+        const f16x2_t d = (v - fz[t]) * fs[t];
+        bq[u] = d[0];
+        bq[u + 1] = d[1];
+      }
+#pragma unroll
+      for (int i = 0; i < kMH; ++i)
+        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bq, acc[i][t], 0, 0, 0);
+    }
+  };
+
+  // Two steps per barrier: their LDS reads and dequantisation overlap each
+  // other's MFMAs, and half as many barriers.
+  for (int s = 0; s < steps; s += 2) {
+    // Steps s and s + 1 have landed once no more than the later steps' DMAs
+    // are in flight.
+    if (s + kRing - 3 < steps) {
+      if (per_step == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm((kRing - 4) * 1));
+      else if (per_step == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm((kRing - 4) * 2));
+    } else {
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    }
+    __builtin_amdgcn_s_barrier();
+    // into the slots steps s - 2 and s - 1 used
+    if (s + kRing - 2 < steps) issue(s + kRing - 2);
+    if (s + kRing - 1 < steps) issue(s + kRing - 1);
+    compute(s);
+    if (s + 1 < steps) compute(s + 1);
+  }
+
+  // ---- epilogue: element r of acc[i][t] is row 16 (mh kMH + i) + 4 lg + r,
+  // column 8 (chunk*32 + pl) + colt[t] ------------------------------------------
+  const int nbase = chunk * kCols + 8 * pl;
+  if (a.splits > 1) {
+    float* part = a.partial + (int64_t)split * a.M * a.N;
+#pragma unroll
+    for (int i = 0; i < kMH; ++i)
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * (mh * kMH + i) + 4 * lg + r;
+          const int n = nbase + colt[t];
+          if (m < a.M && n < a.N)
+            __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][t][r], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    volatile int* s_last = reinterpret_cast<volatile int*>(smem);  // ring is idle now
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCtrStride], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    // Sum the splits of this chunk in split order: 8 outputs per thread per
+    // round (row-major, 256 consecutive columns per row), 4 splits deep.
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
+    const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
+    constexpr int kO = 8, kSB = 4;
+    const int total = a.M * kCols;
+    for (int base = 0; base < total; base += 512 * kO) {
+      uint32_t off[kO];
+      bool ok[kO];
+      float v[kO];
+#pragma unroll
+      for (int j = 0; j < kO; ++j) {
+        const int e = base + j * 512 + tid;
+        const int m = e / kCols, n = chunk * kCols + e % kCols;
+        ok[j] = e < total && n < a.N;
+        off[j] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 1)) * 4);
+        v[j] = 0.f;
+      }
+      for (int sp = 0; sp < a.splits; sp += kSB) {
+        uint32_t t8[kO][kSB];
+#pragma unroll
+        for (int j = 0; j < kO; ++j)
+#pragma unroll
+          for (int q = 0; q < kSB; ++q)
+            t8[j][q] = __builtin_amdgcn_raw_buffer_load_b32(pres, off[j], (uint32_t)min(sp + q, a.splits - 1) * sstride,
+                                                            kCachePolicySC1);
+#pragma unroll
+        for (int j = 0; j < kO; ++j)
+#pragma unroll
+          for (int q = 0; q < kSB; ++q) v[j] += (sp + q < a.splits) ? __builtin_bit_cast(float, t8[j][q]) : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < kO; ++j) {
+        if (!ok[j]) continue;
+        const int e = base + j * 512 + tid;
+        const int m = e / kCols, n = chunk * kCols + e % kCols;
+        float o = v[j];
+        if (a.bias) o += load_f32_any(a.bias, n, a.bt);
+        store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, o);
+      }
+    }
+    if (tid == 0)
+      __hip_atomic_store(&a.counters[chunk * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int n = nbase + colt[t];
+    if (n >= a.N) continue;
+    const float b = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
+#pragma unroll
+    for (int i = 0; i < kMH; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * (mh * kMH + i) + 4 * lg + r;
+        if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][t][r] + b);
+      }
+  }
+}
+
+int env_int(const char* name, int dflt) {
+  const char* e = std::getenv(name);
+  return e ? std::atoi(e) : dflt;
+}
+
+int64_t cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int v = 0;
+    check_hip(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    cached[dev] = v > 0 ? v : 256;
+  }
+  return cached[dev];
+}
+
+template <int MT>
+void launch_mt(const GemmProblem& p) {
+  constexpr int kXSlot = 16 * MT * 64;
+  const size_t smem = (size_t)kRing * kWSlot + (size_t)kRing * kXSlot + (size_t)kMaxGroups * kPacks * 4 +
+                      (size_t)kMaxGroups * kCols * 4;
+  const int chunks = (int)((p.N + kCols - 1) / kCols);
+  const int total_steps = (int)(p.K / kStep);
+  // About one workgroup per CU, each run at least 8 steps and touching at
+  // most kMaxGroups groups, and fp32 partials (splits x M x N x 4 bytes) at
+  // most half the packed weights (K x N / 2 bytes): split-K traffic and the
+  // final reduction cost more than the extra workgroups gain beyond that.
+  int splits = (int)std::max<int64_t>(1, cu_count() / chunks);
+  splits = std::min(splits, std::max(1, total_steps / 8));
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (16 * p.rows)));
+  if (int v = env_int("AWQ_SKINNY_SPLITS", 0); v >= 1) splits = std::min(v, total_steps);
+  int sps = (total_steps + splits - 1) / splits;
+  while ((int64_t)sps * kStep / p.group + 2 > kMaxGroups) {
+    ++splits;
+    sps = (total_steps + splits - 1) / splits;
+  }
+  splits = (total_steps + sps - 1) / sps;
+  while (splits > 1 && (int64_t)splits * p.rows * p.N * 4 >= (1ll << 32)) {
+    --splits;
+    sps = (total_steps + splits - 1) / splits;
+    splits = (total_steps + sps - 1) / sps;
+  }
+  SkinnyArgs a{};
+  a.x = p.x;
+  a.qweight = p.qweight;
+  a.qzeros = p.qzeros;
+  a.scales = p.scales;
+  a.bias = p.bias;
+  a.y = p.y;
+  a.st = p.st;
+  a.bt = p.bt;
+  a.yt = p.yt;
+  a.M = (int32_t)p.rows;
+  a.K = (int32_t)p.K;
+  a.N = (int32_t)p.N;
+  a.group = (int32_t)p.group;
+  a.splits = splits;
+  a.steps_per_split = sps;
+  a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  if (splits > 1) {
+    a.counters = static_cast<uint32_t*>(
+        workspace_get(p.stream, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));
+    a.partial = static_cast<float*>(
+        workspace_get(p.stream, (size_t)splits * p.rows * p.N * sizeof(float), kWsPartials));
+  }
+  static bool attr_set = false;
+  if (!attr_set) {
+    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)smem),
+              "hipFuncSetAttribute(skinny)");
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((skinny_kernel<MT>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+  check_hip(hipGetLastError(), "skinny kernel launch");
+}
+
+}  // namespace
+
+bool skinny_ok(const GemmProblem& p) {
+  // Wide outputs only: with N < 8192 (fewer than 32 chunks) the K splits
+  // needed to occupy the CUs cost more than the large-tile kernel loses
+  // (measured at 4096 x 4096 and 14336 x 4096). AWQ_SKINNY=1 forces it.
+  const int force = env_int("AWQ_SKINNY", -1);
+  if (force == 0 || (force != 1 && p.N < 8192)) return false;
+  return p.xt == AWQ_F16 && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
+         p.N % 32 == 0 && p.K * (p.N / 8) * 4 < (1ll << 32) && p.rows * p.K * 2 < (1ll << 32) &&
+         (p.K / p.group) * p.N * 4 < (1ll << 32);
+}
+
+void launch_skinny(const GemmProblem& p) {
+  if (p.rows <= 32) return launch_mt<2>(p);
+  if (p.rows <= 64) return launch_mt<4>(p);
+  return launch_mt<8>(p);
+}
+
+}  // namespace cube_awq

@@ -402,3 +402,25 @@ def test_small_m_every_configuration(dev, monkeypatch, rpw):
     x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f32", s_dt="f32")
     y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f32", "f32", "f32")
     assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, None, g, "f32", "f32")) <= TOL_FP32
+
+
+# 17..128 rows of f16 activations run on the skinny kernel (awq_skinny.hip);
+# AWQ_SKINNY=0 sends them to the large-tile kernels.
+@pytest.mark.parametrize("path", ["1", "0"])
+@pytest.mark.parametrize("M", [17, 33, 64, 100, 128])
+def test_skinny_both_paths(dev, monkeypatch, path, M):
+    monkeypatch.setenv("AWQ_SKINNY", path)
+    K, N, g = 2048, 2080, 128  # N % 256 != 0: ragged last chunk
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt="f16", bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f16", "f16", "f32")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, "f16", "f16")) <= TOL_MFMA
+
+
+@pytest.mark.parametrize("splits", [1, 3, 8, 64])
+@pytest.mark.parametrize("s_dt,g", [("f16", 64), ("f32", 128), ("bf16", 256)])
+def test_skinny_every_split(dev, monkeypatch, splits, s_dt, g):
+    monkeypatch.setenv("AWQ_SKINNY_SPLITS", str(splits))
+    M, K, N = 48, 4096, 768
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt=s_dt, bias=True)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f16", s_dt, "f16"))
+    assert oracle.rel_l2(host_f32(y, "f16"), _ref64(x, qw, qz, sc, b, g, "f16", s_dt)) <= TOL_MFMA
