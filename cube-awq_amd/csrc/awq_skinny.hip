@@ -12,18 +12,19 @@
 //  * A workgroup owns 256 columns (32 packed words = 128 bytes of each row)
 //    and a run of K; 32-row steps of W, the matching 32 columns of X and,
 //    up front, the zeros and scales of the run's groups go global -> LDS
-//    directly (buffer_load ... lds, 4 bytes per lane) into a ring of kRing
+//    directly (buffer_load ... lds, 16 bytes per lane for W and X, 4 for the
+//    zeros and scales) into a ring of kRing
 //    steps, kRing - 1 steps ahead, with explicit vmcnt waits and one
 //    s_barrier per step.
-//  * 8 waves: wave w takes packs 8 (w & 3) .. 8 (w & 3) + 7 (64 columns, four
-//    16-column MFMA tiles) for row tiles of 16 in half (w >> 2) of the rows.
+//  * 8 waves: wave w takes packs 4 w .. 4 w + 3 (32 columns, two 16-column
+//    MFMA tiles) for every 16-row tile, so each weight is dequantised once.
 //    Lane (lg = lane / 16, lj = lane % 16) reads the 8 words of rows
-//    8 lg .. 8 lg + 7 of pack 8 (w & 3) + (lj & 7) from LDS and builds the
-//    B operand of tile t from packed lane c = 2 t + (lj >> 3): one v_perm_b32
-//    gathers byte t of two rows, one v_bitop3_b32 makes the f16 magic 1024 + q
+//    8 lg .. 8 lg + 7 of pack 4 w + (lj & 3) from LDS and builds the B operand
+//    of tile t from packed lane c = 4 t + (lj >> 2): one v_perm_b32 gathers
+//    byte c / 2 of two rows, one v_bitop3_b32 makes the f16 magic 1024 + q
 //    (64 + q for the high nibble), then an exact v_pk_add_f16 of -(1024 + z)
 //    and one v_pk_mul_f16 by s: 2 VALU ops per weight.
-//  * Waves never share output rows, so there is no cross-wave reduction; K
+//  * Waves never share outputs, so there is no cross-wave reduction; K
 //    splits (grid.y) publish fp32 partials and the last workgroup to arrive on
 //    a chunk sums them in split order (deterministic), adds the bias and
 //    writes Y.
@@ -82,13 +83,13 @@ __device__ __forceinline__ int xswz(int r) { return (r >> 2) & 3; }
 
 template <int MT>
 __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
-  constexpr int kMH = MT / 2;                  // row tiles per wave
+  constexpr int kT = 2;                        // 16-column MFMA tiles per wave
   constexpr int kXRows = 16 * MT;
   constexpr int kXSlot = kXRows * 64;          // 32 f16 columns of X per row
   // 16-byte DMAs per step: W rows 8 i .. 8 i + 7 by wave i (i < 4); X rows
   // 16 j .. 16 j + 15 by wave 4 + j % 4 (MT of them).
-  constexpr int kXPerWave = MT >= 4 ? MT / 4 : 1;
-  static_assert(MT % 2 == 0 && MT <= 8, "row tiles");
+  constexpr int kXPerWave = (MT + 3) / 4;
+  static_assert(MT >= 2 && MT <= 8, "row tiles");
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* wring = smem;                               // kRing W slots
   unsigned char* xring = smem + kRing * kWSlot;              // kRing X slots
@@ -99,7 +100,6 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lg = lane >> 4, lj = lane & 15;
-  const int cg = wave & 3, mh = wave >> 2;
   const int chunk = blockIdx.x, split = blockIdx.y;
   const int np = a.N >> 3;
   const int s0 = split * a.steps_per_split;
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   // X (waves 4..7): rows 16 j .. 16 j + 15; lane l -> row + (l >> 2), slot l & 3
   // holding granule (l & 3) ^ xswz(row) (16 bytes = 8 f16 columns).
   const int xw = wave - 4;
-  const int n_xins = xw < 0 ? 0 : (MT >= 4 ? kXPerWave : (xw < MT ? 1 : 0));
+  const int n_xins = xw < 0 ? 0 : (MT - xw + 3) / 4;  // tiles xw, xw + 4, ... below MT
   uint32_t xvoff[kXPerWave];
 #pragma unroll
   for (int i = 0; i < kXPerWave; ++i) {
@@ -169,31 +169,36 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   const int pre = min(kRing - 2, steps);
   for (int s = 0; s < pre; ++s) issue(s);
 
-  // ---- per-lane constants -----------------------------------------------------
-  const int pl = 8 * cg + (lj & 7);  // pack within the chunk
-  const int hh = lj >> 3;            // nibble: packed lane c = 2 t + hh
+  // ---- per-lane constants: wave w owns packs 4 w .. 4 w + 3 (32 columns, two
+  // 16-column MFMA tiles) for every row tile; in tile t lane lj is pack
+  // 4 w + (lj & 3), packed lane c = 4 t + (lj >> 2) (byte 2 t + (lj >> 3),
+  // nibble (lj >> 2) & 1), so each weight is dequantised once.
+  const int pl = 4 * wave + (lj & 3);  // pack within the chunk
+  const int hh = (lj >> 2) & 1;        // nibble of the byte
   const bool seq = a.seq != 0;
-  // column within the pack of packed lane c = 2 t + hh
-  int colt[4];
+  int colt[kT];
+  uint32_t selt[kT];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const int c = 2 * t + hh;
+  for (int t = 0; t < kT; ++t) {
+    const int c = 4 * t + (lj >> 2);
     colt[t] = seq ? c : awq_col_of_lane(c);
+    const uint32_t b = (uint32_t)(c >> 1);
+    selt[t] = b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
   }
   const uint32_t hmask = hh ? 0x00F000F0u : 0x000F000Fu;
   const uint32_t hexp = hh ? 0x54005400u : 0x64006400u;
 
-  f32x4_t acc[kMH][4];
+  f32x4_t acc[MT][kT];
 #pragma unroll
-  for (int i = 0; i < kMH; ++i)
+  for (int i = 0; i < MT; ++i)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < kT; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  f16x2_t fz[4], fs[4];
+  f16x2_t fz[kT], fs[kT];
   int cur_g = -1;
 
   // One step: the zero points and scales when the group changes, then the
-  // 8 W words and the A operands from LDS, 4 B operands, 4 kMH MFMAs.
+  // 8 W words and the A operands from LDS, 2 B operands, 2 MT MFMAs.
   auto compute = [&](int s) {
     const int k = (s0 + s) * kStep;
     const int g = k / a.group - g_first;
@@ -201,9 +206,8 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
       cur_g = g;
       const uint32_t zw = zlds[g * kPacks + pl];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const uint32_t sel = (uint32_t)t | (0x0Cu << 8) | ((4u + t) << 16) | (0x0Cu << 24);
-        const uint32_t zh = __builtin_amdgcn_perm(zw, zw, sel);
+      for (int t = 0; t < kT; ++t) {
+        const uint32_t zh = __builtin_amdgcn_perm(zw, zw, selt[t]);
         fz[t] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(zh, hmask, hexp, 0xEA));
         const int col = 8 * pl + colt[t];
         float sv;
@@ -223,26 +227,25 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
       wv[u] = *reinterpret_cast<const uint32_t*>(wsl + (r >> 3) * kWBlock + (r & 7) * 128 + pl * 4);
     }
     const unsigned char* xsl = xring + (s % kRing) * kXSlot;
-    f16x8_t av[kMH];
+    f16x8_t av[MT];
 #pragma unroll
-    for (int i = 0; i < kMH; ++i) {
-      const int r = 16 * (mh * kMH + i) + lj;
+    for (int i = 0; i < MT; ++i) {
+      const int r = 16 * i + lj;
       av[i] = *reinterpret_cast<const f16x8_t*>(xsl + r * 64 + ((lg ^ xswz(r)) << 4));
     }
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const uint32_t sel = (uint32_t)t | (0x0Cu << 8) | ((4u + t) << 16) | (0x0Cu << 24);
+    for (int t = 0; t < kT; ++t) {
       f16x8_t bq;
 #pragma unroll
       for (int u = 0; u < 8; u += 2) {
-        const uint32_t h = __builtin_amdgcn_perm(wv[u + 1], wv[u], sel);
+        const uint32_t h = __builtin_amdgcn_perm(wv[u + 1], wv[u], selt[t]);
         const f16x2_t v = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(h, hmask, hexp, 0xEA));
         const f16x2_t d = (v - fz[t]) * fs[t];
         bq[u] = d[0];
         bq[u + 1] = d[1];
       }
 #pragma unroll
-      for (int i = 0; i < kMH; ++i)
+      for (int i = 0; i < MT; ++i)
         acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bq, acc[i][t], 0, 0, 0);
     }
   };
@@ -266,18 +269,18 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     if (s + 1 < steps) compute(s + 1);
   }
 
-  // ---- epilogue: element r of acc[i][t] is row 16 (mh kMH + i) + 4 lg + r,
-  // column 8 (chunk*32 + pl) + colt[t] ------------------------------------------
+  // ---- epilogue: element r of acc[i][t] is row 16 i + 4 lg + r, column
+  // 8 (chunk*32 + pl) + colt[t] --------------------------------------------------
   const int nbase = chunk * kCols + 8 * pl;
   if (a.splits > 1) {
     float* part = a.partial + (int64_t)split * a.M * a.N;
 #pragma unroll
-    for (int i = 0; i < kMH; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int t = 0; t < kT; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = 16 * (mh * kMH + i) + 4 * lg + r;
+          const int m = 16 * i + 4 * lg + r;
           const int n = nbase + colt[t];
           if (m < a.M && n < a.N)
             __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][t][r], __ATOMIC_RELAXED,
@@ -339,15 +342,15 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     return;
   }
 #pragma unroll
-  for (int t = 0; t < 4; ++t) {
+  for (int t = 0; t < kT; ++t) {
     const int n = nbase + colt[t];
     if (n >= a.N) continue;
     const float b = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
 #pragma unroll
-    for (int i = 0; i < kMH; ++i)
+    for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int m = 16 * (mh * kMH + i) + 4 * lg + r;
+        const int m = 16 * i + 4 * lg + r;
         if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][t][r] + b);
       }
   }
@@ -378,13 +381,16 @@ void launch_mt(const GemmProblem& p) {
                       (size_t)kMaxGroups * kCols * 4;
   const int chunks = (int)((p.N + kCols - 1) / kCols);
   const int total_steps = (int)(p.K / kStep);
-  // About one workgroup per CU, each run at least 8 steps and touching at
-  // most kMaxGroups groups, and fp32 partials (splits x M x N x 4 bytes) at
-  // most half the packed weights (K x N / 2 bytes): split-K traffic and the
-  // final reduction cost more than the extra workgroups gain beyond that.
+  // About one workgroup per CU, each run at least 16 steps and touching at
+  // most kMaxGroups groups; fp32 partials (splits x M x N x 4 bytes) at most
+  // the packed weights (K x N / 2 bytes), and at most 1024 partial rows per
+  // chunk for the last workgroup to sum (splits x M): beyond those the split-K
+  // traffic and the serial reduction cost more than the extra workgroups gain
+  // (measured on 4096..14336-deep, 4096..28672-wide problems, 32..128 rows).
   int splits = (int)std::max<int64_t>(1, cu_count() / chunks);
-  splits = std::min(splits, std::max(1, total_steps / 8));
-  splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (16 * p.rows)));
+  splits = std::min(splits, std::max(1, total_steps / 16));
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (8 * p.rows)));
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, 1024 / p.rows));
   if (int v = env_int("AWQ_SKINNY_SPLITS", 0); v >= 1) splits = std::min(v, total_steps);
   int sps = (total_steps + splits - 1) / splits;
   while ((int64_t)sps * kStep / p.group + 2 > kMaxGroups) {
@@ -434,11 +440,11 @@ void launch_mt(const GemmProblem& p) {
 }  // namespace
 
 bool skinny_ok(const GemmProblem& p) {
-  // Wide outputs only: with N < 8192 (fewer than 32 chunks) the K splits
-  // needed to occupy the CUs cost more than the large-tile kernel loses
-  // (measured at 4096 x 4096 and 14336 x 4096). AWQ_SKINNY=1 forces it.
+  // Faster than the large-tile kernels at 17..128 rows for every measured
+  // shape with N >= 1024 (K 4096..28672, N 1024..28672: 1.0-2.0x); narrower
+  // outputs stay on them. AWQ_SKINNY=0/1 forces the choice.
   const int force = env_int("AWQ_SKINNY", -1);
-  if (force == 0 || (force != 1 && p.N < 8192)) return false;
+  if (force == 0 || (force != 1 && p.N < 1024)) return false;
   return p.xt == AWQ_F16 && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
          p.N % 32 == 0 && p.K * (p.N / 8) * 4 < (1ll << 32) && p.rows * p.K * 2 < (1ll << 32) &&
          (p.K / p.group) * p.N * 4 < (1ll << 32);
@@ -446,7 +452,9 @@ bool skinny_ok(const GemmProblem& p) {
 
 void launch_skinny(const GemmProblem& p) {
   if (p.rows <= 32) return launch_mt<2>(p);
+  if (p.rows <= 48) return launch_mt<3>(p);
   if (p.rows <= 64) return launch_mt<4>(p);
+  if (p.rows <= 96) return launch_mt<6>(p);
   return launch_mt<8>(p);
 }
 

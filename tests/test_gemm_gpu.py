@@ -407,7 +407,7 @@ def test_small_m_every_configuration(dev, monkeypatch, rpw):
 # 17..128 rows of f16 activations run on the skinny kernel (awq_skinny.hip);
 # AWQ_SKINNY=0 sends them to the large-tile kernels.
 @pytest.mark.parametrize("path", ["1", "0"])
-@pytest.mark.parametrize("M", [17, 33, 64, 100, 128])
+@pytest.mark.parametrize("M", [17, 33, 48, 64, 80, 96, 100, 128])
 def test_skinny_both_paths(dev, monkeypatch, path, M):
     monkeypatch.setenv("AWQ_SKINNY", path)
     K, N, g = 2048, 2080, 128  # N % 256 != 0: ragged last chunk
