@@ -11,7 +11,10 @@ measured read-stream ceiling (a plain streaming-read kernel from the bench
 helper library over buffers of the decode call's size); prefill at M=2048 on
 the same shape (fp16 activations, fp16 MFMA, fp32 accumulation; TFLOP/s of
 2*M*N*K), with M=16, 64, 512 beside it; the standalone dequantize of K=14336,
-N=4096, g64 (f32 out; GB/s of read+write).
+N=4096, g64 (f32 out; GB/s of read+write); the gate and up projections of the
+same shape with SiLU(gate) * up as one awq_gemm_silu_mul launch against the
+unfused sequence (two awq_gemm launches and torch's SiLU and multiply) at
+M = 1, 16, 64.
 
 Method: inputs resident in HBM before timing; the decode rotates over
 ceil(512 MB / bytes-per-call) independent weight copies so the 256 MB MALL
@@ -187,6 +190,54 @@ def main():
             del bufs
         del ws
 
+        if args.only is None:
+            # Llama-3-8B MLP input half, gate and up 4096 -> 14336 each: one
+            # awq_gemm_silu_mul launch over the column-interleaved weights
+            # (28672 wide) against the unfused sequence (two awq_gemm launches
+            # and torch's SiLU * up), both on rotated weight copies.
+            NI = 2 * N
+            gu_bytes = K * NI // 2 + (K // G) * (NI // 8) * 4 + (K // G) * NI * 2
+            gcopies = math.ceil(512e6 / gu_bytes)
+            fqw = torch.from_numpy(synth.packed_nibbles(synth.TID_QWEIGHT, K, NI // 8).view(np.int32)).to(dev)
+            fqz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, K // G, NI // 8).view(np.int32)).to(dev)
+            fsc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (K // G, NI), 0.002, 0.02, np.float16)).to(dev)
+            h = N // 8
+            # per copy: the fused tensors, then gate and up (halves of the same
+            # columns) as separate contiguous tensors for the unfused sequence
+            gw = [(fqw.clone(), fqz.clone(), fsc.clone(),
+                   fqw[:, :h].contiguous(), fqz[:, :h].contiguous(), fsc[:, :N].contiguous(),
+                   fqw[:, h:].contiguous(), fqz[:, h:].contiguous(), fsc[:, N:].contiguous())
+                  for _ in range(gcopies)]
+            del fqw, fqz, fsc
+            out["gate_up_silu"] = {}
+            for mr, xdt in ((1, np.float32), (16, np.float16), (64, np.float16)):
+                xt = _lib.AWQ_F32 if xdt == np.float32 else _lib.AWQ_F16
+                tdt = torch.float32 if xdt == np.float32 else torch.float16
+                xr = torch.from_numpy(synth.normal(synth.TID_X, (mr, K), xdt)).to(dev)
+                yf = torch.empty((mr, N), dtype=tdt, device=dev)
+                yg = torch.empty((mr, N), dtype=tdt, device=dev)
+                yu = torch.empty((mr, N), dtype=tdt, device=dev)
+                ys = torch.empty((mr, N), dtype=tdt, device=dev)
+
+                def fused(i, xr=xr, yf=yf, mr=mr, xt=xt):
+                    w = gw[i % gcopies]
+                    rc = L.awq_gemm_silu_mul(xr.data_ptr(), xt, w[0].data_ptr(), w[1].data_ptr(), w[2].data_ptr(),
+                                             _lib.AWQ_F16, None, _lib.AWQ_F32, yf.data_ptr(), xt, mr, K, NI, G,
+                                             cur_stream())
+                    if rc:
+                        _lib.check(rc)
+
+                def unfused(i, xr=xr, yg=yg, yu=yu, ys=ys, mr=mr, xt=xt):
+                    w = gw[i % gcopies]
+                    call_gemm(xr, xt, w[3], w[4], w[5], _lib.AWQ_F16, yg, xt, mr, K, N, G)
+                    call_gemm(xr, xt, w[6], w[7], w[8], _lib.AWQ_F16, yu, xt, mr, K, N, G)
+                    torch.mul(torch.nn.functional.silu(yg), yu, out=ys)
+
+                fms, _, _ = graph_time(fused, 50, 20, 500)
+                ums, _, _ = graph_time(unfused, 50, 20, 500)
+                out["gate_up_silu"][mr] = dict(fused_us=fms * 1e3, unfused_us=ums * 1e3)
+            del gw
+
     # ---------------- prefill M=2048, 4096 -> 14336 ---------------------------------------
     PM = 2048
     pf_flops = 2.0 * PM * N * K
@@ -335,6 +386,11 @@ def main():
                                 "dtype": "f16 in, fp32 accumulate, f16 out", "calls": p["calls"]}
         if "dense_tflops" in p:
             res["prefill_m2048"]["dense_fp16_library_gemm_tflops"] = round(p["dense_tflops"], 2)
+    if "gate_up_silu" in out:
+        res["gate_up_silu_4096x2x14336"] = {
+            f"M={m}": {"fused_us": round(v["fused_us"], 2), "unfused_us": round(v["unfused_us"], 2),
+                       "speedup": round(v["unfused_us"] / v["fused_us"], 2)}
+            for m, v in out["gate_up_silu"].items()}
     if "prefill_rows" in out:
         res["prefill_rows_4096x14336"] = {
             f"M={m}": {"us_per_call": round(v["us"], 2), "tflops": round(v["tflops"], 1)}

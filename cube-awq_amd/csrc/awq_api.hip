@@ -441,7 +441,7 @@ int awq_dequantize_native(const awq_tensor_ref* q_weight, const awq_tensor_ref* 
 static int gemm_entry(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
                       const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
                       int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
-                      int32_t order, void* stream) {
+                      int32_t order, int32_t act, void* stream) {
   return guarded([&] {
     AWQ_ASSERT(M >= 0 && K >= 0 && N >= 0, "shape sizes must be non-negative");
     awq_shape_config s = awq_shape_config_new(M, N, K, select_tile_m(M), select_tile_n(N), kInnerK);
@@ -455,6 +455,7 @@ static int gemm_entry(const void* x, int32_t x_t, const uint32_t* qweight, const
     if (bias) check_float_dtype(b_t, "bias");
     if (order == AWQ_ORDER_SEQUENTIAL)
       AWQ_ASSERT(s_t == x_t, "sequential-order GEMM needs scales in the input dtype");
+    if (act) AWQ_ASSERT(N % 64 == 0, "gate/up GEMM: N (gate and up interleaved) must be a multiple of 64");
     GemmProblem p{};
     p.x = x;
     p.xt = x_t;
@@ -471,6 +472,7 @@ static int gemm_entry(const void* x, int32_t x_t, const uint32_t* qweight, const
     p.N = N;
     p.group = group_size;
     p.order = order;
+    p.act = act;
     p.stream = static_cast<hipStream_t>(stream);
     run_gemm(p, M);
   });
@@ -480,7 +482,15 @@ int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t
              const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
              int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream) {
   return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
-                    AWQ_ORDER_AUTOAWQ, stream);
+                    AWQ_ORDER_AUTOAWQ, 0, stream);
+}
+
+int awq_gemm_silu_mul(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                      const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                      int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                      void* stream) {
+  return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
+                    AWQ_ORDER_AUTOAWQ, 1, stream);
 }
 
 int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
@@ -488,7 +498,7 @@ int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const 
                      int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
                      int32_t order, void* stream) {
   return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
-                    order, stream);
+                    order, 0, stream);
 }
 
 int awq_validate_gemm(int64_t M, int64_t K, int64_t N, int64_t group_size) {

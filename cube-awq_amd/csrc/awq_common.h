@@ -93,6 +93,20 @@ __device__ __forceinline__ void store_f32_any(void* p, int64_t i, int32_t t, flo
   else ((bf16_t*)p)[i] = from_f32<bf16_t>(v);
 }
 
+// Fused gate/up epilogue: the weights interleave the two projections by
+// column (column 2j = gate j, column 2j + 1 = up j); output j is SiLU(gate j)
+// * up j, SiLU(g) = g / (1 + e^-g), in a [rows, N/2] output.
+__device__ __forceinline__ float silu_mul(float g, float u) { return g / (1.f + __expf(-g)) * u; }
+
+// Final store of output (m, n) of a width-N GEMM: v itself, or with the
+// activation (act != 0) SiLU(v) * partner from the lane of the even column
+// of a pair, to (m, n / 2); the odd column's lane stores nothing.
+__device__ __forceinline__ void store_out(void* y, int32_t yt, int32_t act, int64_t m, int64_t n,
+                                          int64_t N, float v, float partner) {
+  if (!act) store_f32_any(y, m * N + n, yt, v);
+  else if ((n & 1) == 0) store_f32_any(y, m * (N >> 1) + (n >> 1), yt, silu_mul(v, partner));
+}
+
 // Packed lane L of two words as f16x2 magic numbers: the byte holding lane L
 // of w0 and of w1 goes to the two halves (v_perm_b32), then one v_bitop3
 // keeps the nibble and ORs in the exponent: low nibble (even L) -> 0x6400 | q
@@ -156,6 +170,7 @@ struct GemmProblem {
   int64_t rows;  // rows to compute and write (m_valid)
   int64_t K, N, group;
   int32_t order;  // AWQ_ORDER_AUTOAWQ (awq_gemm) or AWQ_ORDER_SEQUENTIAL (AWQLinear's weights)
+  int32_t act;    // 1: gate/up interleaved by column, y [rows, N/2] = SiLU(gate) * up
   hipStream_t stream;
 };
 

@@ -88,6 +88,7 @@ struct GemmArgs {
   int32_t splits, stages_per_split;
   float* partial;
   uint32_t* counters;
+  int32_t act;  // gate/up SiLU epilogue (store_out)
 };
 
 constexpr int kTileCtrStride = 64;  // u32 words between per-tile counters (256 B)
@@ -347,6 +348,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
 
   // ---- epilogue: D layout of a 32x32 MFMA: lane l, register r ->
   //      row 8*(r/4) + 4*(l/32) + r%4, column l%32 ----------------------------
+  // Column lane % 32: a gate/up pair is this lane and its xor-1 neighbour
+  // (N is even, so both are in range or neither).
 #pragma unroll
   for (int j = 0; j < C::kJ; ++j) {
     const int n = n0 + bcol + 32 * j;
@@ -357,7 +360,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][j][r] + bias);
+        const float v = acc[i][j][r] + bias;
+        const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
+        if (m < a.M) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
       }
     }
   }
@@ -811,17 +816,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
           for (int q = 0; q < 4; ++q) v[q] += ok ? __builtin_bit_cast(float, t8[j][q]) : 0.f;
         }
       }
+      // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        float o = v[q];
-        if (a.bias) o += load_f32_any(a.bias, n + q, a.bt);
-        store_f32_any(a.y, (int64_t)m * a.N + n + q, a.yt, o);
-      }
+      for (int q = 0; q < 4; ++q)
+        if (a.bias) v[q] += load_f32_any(a.bias, n + q, a.bt);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, a.act, m, n + q, a.N, v[q], v[q ^ 1]);
     }
     if (tid == 0)
       __hip_atomic_store(&a.counters[t * kTileCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
+  // Column lane % 32 (or % 16): a gate/up pair is this lane and its xor-1
+  // neighbour (N is even, so both are in range or neither).
 #pragma unroll
   for (int j = 0; j < C::kJ; ++j) {
     const int n = out_col(j);
@@ -832,7 +839,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 #pragma unroll
       for (int r = 0; r < kAccN; ++r) {
         const int m = out_row(i, r);
-        if (m < a.M) store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, acc[i][j][r] + bias);
+        const float v = acc[i][j][r] + bias;
+        const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
+        if (m < a.M) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
       }
     }
   }
@@ -868,6 +877,7 @@ void launch_big(const GemmProblem& p, int splits) {
   a.st = p.st;
   a.bt = p.bt;
   a.yt = p.yt;
+  a.act = p.act;
   a.M = (int32_t)p.rows;
   a.K = (int32_t)p.K;
   a.N = (int32_t)p.N;
@@ -914,6 +924,7 @@ void launch_cfg(const GemmProblem& p) {
   a.st = p.st;
   a.bt = p.bt;
   a.yt = p.yt;
+  a.act = p.act;
   a.M = (int32_t)p.rows;
   a.K = (int32_t)p.K;
   a.N = (int32_t)p.N;

@@ -56,6 +56,7 @@ struct GemvArgs {
   int32_t K, N, group;
   int32_t splits;
   int32_t seq;        // sequential nibble order (packed lane j = column j)
+  int32_t act;        // gate/up SiLU epilogue (store_out)
 };
 
 template <int XT>
@@ -350,16 +351,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
                          __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
+  // and its xor-1 neighbour.
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int o = threadIdx.x + i * 64 * WAVES;
     const int m = o / kChunkCols, c = o % kChunkCols;
     const int n = col_base + c;
-    if (o < kOut && m < rows && n < a.N) {
-      float v = res[i];
-      if (a.bias) v += load_f32_any(a.bias, n, a.bt);
-      store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, v);
-    }
+    float v = res[i];
+    if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
+    const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
+    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
   }
 }
 
@@ -671,16 +673,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
                          __HIP_MEMORY_SCOPE_AGENT);
   }
 
+  // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
+  // and its xor-1 neighbour.
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
     const int o = threadIdx.x + i * 64 * WAVES;
     const int m = o / kChunkCols, c = o % kChunkCols;
     const int n = col_base + c;
-    if (o < kOut && m < rows && n < a.N) {
-      float v = res[i];
-      if (a.bias) v += load_f32_any(a.bias, n, a.bt);
-      store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, v);
-    }
+    float v = res[i];
+    if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
+    const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
+    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
   }
 }
 
@@ -712,6 +715,7 @@ void launch_cfg(const GemmProblem& p) {
   a.group = (int32_t)p.group;
   a.splits = splits;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  a.act = p.act;
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MT * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
@@ -796,6 +800,7 @@ void launch_mfma_cfg(const GemmProblem& p) {
   a.group = (int32_t)p.group;
   a.splits = splits;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  a.act = p.act;
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);

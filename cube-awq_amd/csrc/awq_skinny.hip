@@ -64,6 +64,7 @@ struct SkinnyArgs {
   int32_t M, K, N, group;
   int32_t splits, steps_per_split;
   int32_t seq;         // sequential nibble order
+  int32_t act;         // gate/up SiLU epilogue (store_out); AutoAWQ order only
 };
 
 constexpr int waitcnt_vm(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -349,18 +350,36 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
           for (int q = 0; q < kSB; ++q) v[j] += (sp + q < a.splits) ? __builtin_bit_cast(float, t8[j][q]) : 0.f;
       }
+      // Adjacent threads hold adjacent columns: a gate/up pair is this lane
+      // and its xor-1 neighbour.
 #pragma unroll
       for (int j = 0; j < kO; ++j) {
-        if (!ok[j]) continue;
         const int e = base + j * 512 + tid;
         const int m = e / kCols, n = chunk * kCols + e % kCols;
         float o = v[j];
-        if (a.bias) o += load_f32_any(a.bias, n, a.bt);
-        store_f32_any(a.y, (int64_t)m * a.N + n, a.yt, o);
+        if (a.bias && ok[j]) o += load_f32_any(a.bias, n, a.bt);
+        const float po = a.act ? __shfl_xor(o, 1, 64) : 0.f;
+        if (ok[j]) store_out(a.y, a.yt, a.act, m, n, a.N, o, po);
       }
     }
     if (tid == 0)
       __hip_atomic_store(&a.counters[chunk * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+  if (a.act) {
+    // AutoAWQ order: tiles 0 and 1 of a lane hold packed lanes q and q + 4 of
+    // its pack, i.e. columns 2 q and 2 q + 1 -- a gate/up pair.
+    const int n = nbase + colt[0];
+    if (n >= a.N) return;
+    const float b0 = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
+    const float b1 = a.bias ? load_f32_any(a.bias, n + 1, a.bt) : 0.f;
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + 4 * lg + r;
+        if (m < a.M) store_out(a.y, a.yt, 1, m, n, a.N, acc[i][0][r] + b0, acc[i][1][r] + b1);
+      }
     return;
   }
 #pragma unroll
@@ -442,6 +461,7 @@ void launch_mt(const GemmProblem& p) {
   a.splits = splits;
   a.steps_per_split = sps;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  a.act = p.act;
   if (splits > 1) {
     a.counters = static_cast<uint32_t*>(
         workspace_get(p.stream, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));

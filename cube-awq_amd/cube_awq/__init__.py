@@ -7,5 +7,6 @@ from ._lib import HipError, LIB_PATH, Panic, lib  # noqa: F401
 from .kernel import (  # noqa: F401
     DECODE_M_THRESHOLD, DECODE_TILE_M, ShapeConfig, awq_gemm_linear, dequantize_awq,
     dequantize_native, validate_decode_launch_params, validate_launch_params)
-from .modules import AWQGEMMLinear, AWQGEMMLinearConfig, AWQLinear, AWQLinearConfig  # noqa: F401
+from .modules import (  # noqa: F401
+    AWQGateUpSiLU, AWQGEMMLinear, AWQGEMMLinearConfig, AWQLinear, AWQLinearConfig)
 from . import checkpoint, pack  # noqa: F401

@@ -17,7 +17,7 @@ them as uint32.
 import torch
 
 from ._lib import Panic
-from .modules import AWQ_PACK_FACTOR, INNER_K, TILE_N_BASE, AWQGEMMLinear, AWQLinear
+from .modules import AWQ_PACK_FACTOR, INNER_K, TILE_N_BASE, AWQGateUpSiLU, AWQGEMMLinear, AWQLinear
 
 _PACKED_DTYPES = (torch.int32, torch.uint32) if hasattr(torch, "uint32") else (torch.int32,)
 
@@ -127,6 +127,19 @@ def load_fused_awq_gemm_linear(source, prefixes, device=None, scale_dtype=None):
     layer = AWQGEMMLinear(qweight.contiguous().to(device), qzeros.contiguous().to(device),
                           scales.contiguous().to(device), None if bias is None else bias.contiguous().to(device))
     return layer, [p[6] for p in parts]
+
+
+def load_awq_gate_up_silu(source, gate_prefix, up_prefix, device=None, scale_dtype=None):
+    """`AWQGateUpSiLU` from the gate and up projections' tensors (e.g.
+    `model.layers.0.mlp.gate_proj` / `.up_proj`): forward(x) = SiLU(gate(x)) *
+    up(x) in one launch. Both must share K, the group size and the width."""
+    gate = load_awq_gemm_linear(source, gate_prefix, None, scale_dtype)
+    up = load_awq_gemm_linear(source, up_prefix, None, scale_dtype)
+    layer = AWQGateUpSiLU.from_gate_up(gate, up)
+    if layer.scales.shape[1] % 64 != 0:
+        raise Panic("gate/up GEMM: N (gate and up interleaved) must be a multiple of 64")
+    return AWQGateUpSiLU(layer.qweight.to(device), layer.qzeros.to(device), layer.scales.to(device),
+                         None if layer.bias is None else layer.bias.to(device))
 
 
 def load_awq_linear(source, prefix, device=None, scale_dtype=None):

@@ -124,6 +124,73 @@ class AWQGEMMLinear:
     __call__ = forward
 
 
+class AWQGateUpSiLU:
+    """Gate and up projections with the SiLU activation in one launch:
+    forward(x) = SiLU(x.Wg + bg) * (x.Wu + bu), SiLU(g) = g / (1 + e^-g), the
+    MLP input half of Llama-style blocks. Not a reference module: the
+    reference runs gate and up as two AWQGEMMLinear forwards (each a GEMM plus
+    a bias op, src/modules/awq_gemm.rs:146-232) and leaves the activation to
+    the caller. The parameters hold the two projections interleaved by column
+    (column 2j = gate j, 2j + 1 = up j; see `from_gate_up`), so the GEMM
+    epilogue has both values of an output in one place."""
+
+    def __init__(self, qweight, qzeros, scales, bias=None):
+        self.qweight = qweight
+        self.qzeros = qzeros
+        self.scales = scales
+        self.bias = bias
+
+    @classmethod
+    def from_gate_up(cls, gate, up):
+        """From two AWQGEMMLinear layers of the same input (same K, group and
+        intermediate width); a missing bias counts as zero."""
+        from .pack import interleave_columns, interleave_packed
+        if tuple(gate.qweight.shape) != tuple(up.qweight.shape) or tuple(gate.scales.shape) != tuple(up.scales.shape):
+            raise Panic("gate and up projections must have the same shapes")
+        if gate.scales.dtype != up.scales.dtype:
+            raise Panic("gate and up scales must share a dtype")
+        bias = None
+        if gate.bias is not None or up.bias is not None:
+            zg = torch.zeros_like(gate.scales[0])
+            bg = gate.bias if gate.bias is not None else zg
+            bu = up.bias if up.bias is not None else zg
+            bias = interleave_columns(bg[None, :], bu[None, :].to(bg.dtype))[0].contiguous()
+        return cls(interleave_packed(gate.qweight, up.qweight).contiguous(),
+                   interleave_packed(gate.qzeros, up.qzeros).contiguous(),
+                   interleave_columns(gate.scales, up.scales).contiguous(), bias)
+
+    def group_size(self):
+        return self.qweight.shape[0] // self.scales.shape[0]
+
+    def forward(self, input, stream=None):
+        """input [..., K] (D >= 2) -> [..., N/2], N the interleaved width."""
+        if input.dim() < 2:
+            raise Panic("input tensor must have at least 2 dims: [..., K]")
+        dims = list(input.shape)
+        k = dims[-1]
+        m = input.numel() // k if k > 0 else 0
+        x = input.reshape(m, k)
+        if not x.is_contiguous():
+            x = x.contiguous()
+        _assert_eq(k, self.qweight.shape[0], "input last dim (K) must match qweight rows")
+        n = self.qweight.shape[-1] * 8
+        out = torch.empty((m, n // 2), dtype=input.dtype, device=input.device)
+        bias = self.bias
+        check(lib().awq_gemm_silu_mul(
+            x.data_ptr(), _lib.awq_dtype(x),
+            self.qweight.data_ptr(), self.qzeros.data_ptr(),
+            self.scales.data_ptr(), _lib.awq_dtype(self.scales),
+            bias.data_ptr() if bias is not None else None,
+            _lib.awq_dtype(bias) if bias is not None else _lib.AWQ_F32,
+            out.data_ptr(), _lib.awq_dtype(out),
+            m, k, n, self.group_size(),
+            stream_ptr(stream, input.device if input.is_cuda else None)))
+        dims[-1] = n // 2
+        return out.reshape(dims)
+
+    __call__ = forward
+
+
 class AWQLinearConfig:
     def __init__(self, d_input, d_output, group_size):
         self.d_input = d_input

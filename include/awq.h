@@ -131,6 +131,20 @@ int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const 
                      int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
                      int32_t order, void* stream);
 
+/* Fused gate/up projection with its activation in the GEMM epilogue: the
+ * weights hold the gate and up projections interleaved by column (column 2j
+ * of qweight/qzeros/scales/bias is gate column j, column 2j + 1 is up column
+ * j; N = 2 x the intermediate width, N % 64 == 0) in AutoAWQ nibble order,
+ * and y [M, N/2] receives SiLU(x.Wg + bg) * (x.Wu + bu), SiLU(g) = g / (1 +
+ * exp(-g)). No reference counterpart: its GEMM path has no activation and
+ * adds the bias as a separate op (src/modules/awq_gemm.rs:225-228), so gate,
+ * up and SiLU * up there are separate launches. Otherwise the constraints and
+ * dispatch of awq_gemm. */
+int awq_gemm_silu_mul(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                      const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                      int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                      void* stream);
+
 /* Host-only check of an awq_gemm problem: the same shape validation awq_gemm
  * applies (the module's constraints through validate_launch_params_impl,
  * src/kernel/awq_kernel_gemm.rs:89-171, with the M <= 8 decode split of :691),

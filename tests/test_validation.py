@@ -319,3 +319,25 @@ def test_validate_gemm_accepts_module_shapes(M, K, N, g):
     L = cube_awq.lib()
     assert L.awq_validate_gemm(M, K, N, g) == 0
     assert L.awq_last_error().decode() == ""
+
+
+def test_silu_mul_rejects_width_not_multiple_of_64():
+    L = cube_awq.lib()
+    rc = L.awq_gemm_silu_mul(None, _lib.AWQ_F32, None, None, None, _lib.AWQ_F16, None, 0, None,
+                             _lib.AWQ_F32, 1, 64, 96, 64, None)
+    assert rc == _lib.AWQ_ERR_INVALID
+    assert "N (gate and up interleaved) must be a multiple of 64" in L.awq_last_error().decode()
+
+
+def test_interleave_packed_round_trip():
+    import numpy as np
+    import torch
+    from cube_awq import pack
+    rng = np.random.default_rng(3)
+    a, b = rng.integers(0, 16, (9, 64)), rng.integers(0, 16, (9, 64))
+    w = pack.interleave_packed(pack.pack(a, "awq"), pack.pack(b, "awq"))
+    nib = pack.unpack(w, "awq")
+    assert np.array_equal(nib[:, 0::2], a) and np.array_equal(nib[:, 1::2], b)
+    t = pack.interleave_packed(torch.from_numpy(pack.pack(a, "awq").view(np.int32)),
+                               torch.from_numpy(pack.pack(b, "awq").view(np.int32)))
+    assert t.dtype == torch.int32 and np.array_equal(t.numpy().view(np.uint32), w)
