@@ -558,16 +558,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
         }
       }
     }
-    float sl[8];
+    float sl[8], slp[8];
     scales_to_f32(sraw[s], a.st, sl);  // column order
+    // Partial sums stay in packed-lane (slot) order; the scale of slot c is
+    // that of its column (c in sequential order, kAwqColOfLane[c] in AutoAWQ).
+#pragma unroll
+    for (int c = 0; c < 8; ++c) slp[c] = seq ? sl[c] : sl[awq_col_of_lane(c)];
     float o[4][8];
 #pragma unroll
     for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = seq ? acc[j][r] : acc[awq_lane_of_col(j)][r];
-        o[r][j] = v * sl[j] * xdown[r];
-      }
+      for (int c = 0; c < 8; ++c) o[r][c] = acc[c][r] * slp[c] * xdown[r];
     auto store = [&](bool add) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -609,8 +610,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
     float v = 0.f;
     if (o < kOut) {
       const int m = o / kChunkCols, c = o % kChunkCols;
+      // column c of its pack sits in slot c (sequential) or kAwqLaneOfCol[c]
+      // = (c >> 1) + 4 (c & 1) (AutoAWQ)
+      const int cs = (c & ~7) | (seq ? (c & 7) : ((c & 7) >> 1) + 4 * (c & 1));
 #pragma unroll
-      for (int ww = 0; ww < kSlots; ++ww) v += red[ww][m][c];
+      for (int ww = 0; ww < kSlots; ++ww) v += red[ww][m][cs];
     }
     res[i] = v;
   }
