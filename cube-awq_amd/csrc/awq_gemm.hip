@@ -791,37 +791,66 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     __syncthreads();
     if (!*s_last) return;
     // 4 consecutive columns per thread and step (N % 8 == 0 keeps a group of
-    // 4 inside the row), agent-scope (sc1) loads, 8 splits in flight.
+    // 4 inside the row) as one 16-byte agent-scope (sc1) load per split, kG
+    // steps at a time with 8 splits each: 8 kG loads in flight per thread.
+    // (One step at a time left this single workgroup latency-bound on the
+    // splits x tile partials: ~30 us for a 128 x 128 tile and 8 splits.)
+    // Every slot is loaded (indices clamped into the workspace) and only the
+    // valid ones are added and stored, so nothing read is ever undefined.
     const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
     const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
-    for (int e = tid * 4; e < BM * BN; e += C::kThreads * 4) {
-      const int m = m0 + e / BN, n = n0 + e % BN;
-      if (m >= a.M || n >= a.N) continue;
-      const uint32_t off = (uint32_t)(((int64_t)m * a.N + n) * 4);
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int s0 = 0; s0 < a.splits; s0 += 8) {
-        // Every slot is loaded (split index clamped) and only the valid ones
-        // are added, so nothing read is ever undefined.
-        uint32_t t8[8][4];
+    constexpr int kG = 4;
+    constexpr int kStep4 = C::kThreads * 4;
+    for (int e0 = tid * 4; e0 < BM * BN; e0 += kG * kStep4) {
+      uint32_t off[kG];
+      bool ok[kG];
+      float v[kG][4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+      for (int g = 0; g < kG; ++g) {
+        const int e = e0 + g * kStep4;
+        const int m = m0 + e / BN, n = n0 + e % BN;
+        ok[g] = e < BM * BN && m < a.M && n < a.N;
+        off[g] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 4)) * 4);
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            t8[j][q] = __builtin_amdgcn_raw_buffer_load_b32(
-                pres, off + 4u * q, (uint32_t)min(s0 + j, a.splits - 1) * sstride, kCachePolicySC1);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const bool ok = s0 + j < a.splits;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) v[q] += ok ? __builtin_bit_cast(float, t8[j][q]) : 0.f;
-        }
+        for (int q = 0; q < 4; ++q) v[g][q] = 0.f;
       }
-      // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
+      for (int s0 = 0; s0 < a.splits; s0 += 8) {
+        float t8[kG][8][4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        if (a.bias) v[q] += load_f32_any(a.bias, n + q, a.bt);
+        for (int g = 0; g < kG; ++g)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, a.act, m, n + q, a.N, v[q], v[q ^ 1]);
+          for (int j = 0; j < 8; ++j) {
+            const u32x4 w4 = __builtin_amdgcn_raw_buffer_load_b128(
+                pres, off[g], (uint32_t)min(s0 + j, a.splits - 1) * sstride, kCachePolicySC1);
+            // Elements through plain scalars: __builtin_bit_cast applied to
+            // a vector element directly reads the wrong element (hipcc 7.2).
+            const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+            t8[g][j][0] = __uint_as_float(e0);
+            t8[g][j][1] = __uint_as_float(e1);
+            t8[g][j][2] = __uint_as_float(e2);
+            t8[g][j][3] = __uint_as_float(e3);
+          }
+#pragma unroll
+        for (int g = 0; g < kG; ++g)
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const bool live = s0 + j < a.splits;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[g][q] += live ? t8[g][j][q] : 0.f;
+          }
+      }
+#pragma unroll
+      for (int g = 0; g < kG; ++g) {
+        if (!ok[g]) continue;
+        const int e = e0 + g * kStep4;
+        const int m = m0 + e / BN, n = n0 + e % BN;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
+        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, a.act, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+      }
     }
     if (tid == 0)
       __hip_atomic_store(&a.counters[t * kTileCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -994,13 +1023,19 @@ void launch_mode(const GemmProblem& p) {
     else if (tiles(128, 256) >= 200) cfg = 3;
     else {
       cfg = 4;  // 128 x 128 tiles, two workgroups per CU
+      const int64_t t = tiles(128, 128);
+      const int64_t stages = p.K / kBK;
       if (p.rows <= 128) {
         // Skinny problems: split K across workgroups until ~320 are in
-        // flight (at most 8 splits, at least 4 stages each). Larger M keeps
-        // one split: its partials would cost more HBM traffic than they save.
-        const int64_t t = tiles(128, 128);
-        const int64_t stages = p.K / kBK;
+        // flight (at most 8 splits, at least 4 stages each).
         splits = (int)std::min<int64_t>({(320 + t - 1) / t, 8, std::max<int64_t>(stages / 4, 1)});
+      } else {
+        // Fewer tiles than CUs: double the K splits while the workgroups
+        // still fit one per CU (at most 8, at least 4 stages each). Measured
+        // at M = 129..1024 on 4096..14336-deep, 1024..8192-wide problems
+        // (e.g. 14336 -> 4096 at M = 256: 175 -> 70 us with 4 splits); odd
+        // split counts and more than one workgroup per CU measured slower.
+        while (splits < 8 && t * splits * 2 <= num_cus() && stages / (splits * 2) >= 4) splits *= 2;
       }
     }
   }

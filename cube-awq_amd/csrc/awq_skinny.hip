@@ -482,11 +482,15 @@ void launch_mt(const GemmProblem& p) {
 }  // namespace
 
 bool skinny_ok(const GemmProblem& p) {
-  // Faster than the large-tile kernels at 17..128 rows for every measured
-  // shape with N >= 1024 (K 4096..28672, N 1024..28672: 1.0-2.0x); narrower
-  // outputs stay on them. AWQ_SKINNY=0/1 forces the choice.
+  // Where it beats the 128 x 128 split-K tiles of the large-tile kernel
+  // (measured at K 4096..28672, N 1024..28672, 17..128 rows): wide outputs,
+  // whose many column chunks fill the CUs with few K splits (up to 2.5x at
+  // N >= 8192), and fewer rows the narrower the output. AWQ_SKINNY=0/1 forces
+  // the choice.
   const int force = env_int("AWQ_SKINNY", -1);
-  if (force == 0 || (force != 1 && p.N < 1024)) return false;
+  const bool wins = p.N >= 16384 || (p.N >= 8192 && p.rows <= 96) || (p.N >= 6144 && p.rows <= 48) ||
+                    (p.N >= 4096 && p.K >= 8192 && p.rows <= 32);
+  if (force == 0 || (force != 1 && !wins)) return false;
   return p.xt == AWQ_F16 && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
          p.N % 32 == 0 && p.K * (p.N / 8) * 4 < (1ll << 32) && p.rows * p.K * 2 < (1ll << 32) &&
          (p.K / p.group) * p.N * 4 < (1ll << 32);
