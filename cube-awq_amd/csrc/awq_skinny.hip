@@ -41,6 +41,7 @@ namespace {
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kCols = 256;          // columns per workgroup (chunk)
 constexpr int kPacks = kCols / 8;   // packed words per row of a chunk
@@ -319,47 +320,65 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     }
     __syncthreads();
     if (!*s_last) return;
-    // Sum the splits of this chunk in split order: 8 outputs per thread per
-    // round (row-major, 256 consecutive columns per row), 4 splits deep.
+    // Sum the splits of this chunk in split order: 4 consecutive columns per
+    // 16-byte load (N % 32 == 0 keeps them inside a row), kG column groups
+    // per thread per round, kSB splits deep -- kG kSB loads in flight, so
+    // most chunks take one round. Slots past the chunk, M or the splits are
+    // loaded clamped and not used.
     const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
     const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
-    constexpr int kO = 8, kSB = 4;
-    const int total = a.M * kCols;
-    for (int base = 0; base < total; base += 512 * kO) {
-      uint32_t off[kO];
-      bool ok[kO];
-      float v[kO];
+    constexpr int kG = 4, kSB = 4;
+    constexpr int kQuads = kCols / 4;
+    const int total4 = a.M * kQuads;
+    for (int base = 0; base < total4; base += 512 * kG) {
+      uint32_t off[kG];
+      bool ok[kG];
+      float v[kG][4];
 #pragma unroll
-      for (int j = 0; j < kO; ++j) {
-        const int e = base + j * 512 + tid;
-        const int m = e / kCols, n = chunk * kCols + e % kCols;
-        ok[j] = e < total && n < a.N;
-        off[j] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 1)) * 4);
-        v[j] = 0.f;
+      for (int g = 0; g < kG; ++g) {
+        const int e4 = base + g * 512 + tid;
+        const int m = e4 / kQuads, n = chunk * kCols + 4 * (e4 % kQuads);
+        ok[g] = e4 < total4 && n < a.N;
+        off[g] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 4)) * 4);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[g][q] = 0.f;
       }
       for (int sp = 0; sp < a.splits; sp += kSB) {
-        uint32_t t8[kO][kSB];
+        float t[kG][kSB][4];
 #pragma unroll
-        for (int j = 0; j < kO; ++j)
+        for (int g = 0; g < kG; ++g)
 #pragma unroll
-          for (int q = 0; q < kSB; ++q)
-            t8[j][q] = __builtin_amdgcn_raw_buffer_load_b32(pres, off[j], (uint32_t)min(sp + q, a.splits - 1) * sstride,
-                                                            kCachePolicySC1);
+          for (int b = 0; b < kSB; ++b) {
+            const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(
+                pres, off[g], (uint32_t)min(sp + b, a.splits - 1) * sstride, kCachePolicySC1);
+            // through plain scalars: __builtin_bit_cast of a vector element
+            // directly reads the wrong element (hipcc 7.2)
+            const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+            t[g][b][0] = __uint_as_float(e0);
+            t[g][b][1] = __uint_as_float(e1);
+            t[g][b][2] = __uint_as_float(e2);
+            t[g][b][3] = __uint_as_float(e3);
+          }
 #pragma unroll
-        for (int j = 0; j < kO; ++j)
+        for (int g = 0; g < kG; ++g)
 #pragma unroll
-          for (int q = 0; q < kSB; ++q) v[j] += (sp + q < a.splits) ? __builtin_bit_cast(float, t8[j][q]) : 0.f;
+          for (int b = 0; b < kSB; ++b) {
+            const bool live = sp + b < a.splits;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) v[g][q] += live ? t[g][b][q] : 0.f;
+          }
       }
-      // Adjacent threads hold adjacent columns: a gate/up pair is this lane
-      // and its xor-1 neighbour.
 #pragma unroll
-      for (int j = 0; j < kO; ++j) {
-        const int e = base + j * 512 + tid;
-        const int m = e / kCols, n = chunk * kCols + e % kCols;
-        float o = v[j];
-        if (a.bias && ok[j]) o += load_f32_any(a.bias, n, a.bt);
-        const float po = a.act ? __shfl_xor(o, 1, 64) : 0.f;
-        if (ok[j]) store_out(a.y, a.yt, a.act, m, n, a.N, o, po);
+      for (int g = 0; g < kG; ++g) {
+        if (!ok[g]) continue;
+        const int e4 = base + g * 512 + tid;
+        const int m = e4 / kQuads, n = chunk * kCols + 4 * (e4 % kQuads);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
+        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
+#pragma unroll
+        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, a.act, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
       }
     }
     if (tid == 0)
@@ -484,12 +503,11 @@ void launch_mt(const GemmProblem& p) {
 bool skinny_ok(const GemmProblem& p) {
   // Where it beats the 128 x 128 split-K tiles of the large-tile kernel
   // (measured at K 4096..28672, N 1024..28672, 17..128 rows): wide outputs,
-  // whose many column chunks fill the CUs with few K splits (up to 2.5x at
-  // N >= 8192), and fewer rows the narrower the output. AWQ_SKINNY=0/1 forces
-  // the choice.
+  // whose many column chunks fill the CUs with few K splits (1.1-2.7x at
+  // N >= 6144), and on narrower ones up to 32 rows (1.1-1.5x), or 64 rows
+  // with K >= 8192. AWQ_SKINNY=0/1 forces the choice.
   const int force = env_int("AWQ_SKINNY", -1);
-  const bool wins = p.N >= 16384 || (p.N >= 8192 && p.rows <= 96) || (p.N >= 6144 && p.rows <= 48) ||
-                    (p.N >= 4096 && p.K >= 8192 && p.rows <= 32);
+  const bool wins = p.N >= 6144 || (p.N >= 1024 && (p.rows <= 32 || (p.rows <= 64 && p.K >= 8192)));
   if (force == 0 || (force != 1 && !wins)) return false;
   return p.xt == AWQ_F16 && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
          p.N % 32 == 0 && p.K * (p.N / 8) * 4 < (1ll << 32) && p.rows * p.K * 2 < (1ll << 32) &&
