@@ -193,6 +193,19 @@ static std::map<WsKey, WsBuf>& ws_map() {
   return *m;
 }
 
+int64_t device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int v = 0;
+    check_hip(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
+    cached[dev] = v > 0 ? v : 256;
+  }
+  return cached[dev];
+}
+
 void* workspace_get(hipStream_t stream, size_t bytes, int slot) {
   int dev = 0;
   check_hip(hipGetDevice(&dev), "hipGetDevice");

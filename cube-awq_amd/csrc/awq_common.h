@@ -198,6 +198,9 @@ bool small_m_mfma_ok(const GemmProblem& p, int64_t launch_m);
 bool skinny_ok(const GemmProblem& p);
 void launch_skinny(const GemmProblem& p);
 
+// Compute units of the current device (queried once per device).
+int64_t device_cus();
+
 // Per-(device, stream, slot) device workspace, grown on demand and never shrunk.
 // kWsCounters is zero-filled when (re)allocated and kernels leave it zero;
 // kWsPartials holds split-K partial sums (contents undefined between calls).

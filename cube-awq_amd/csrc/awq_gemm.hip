@@ -876,8 +876,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 }
 
-int64_t num_cus();
-
 // Row tiles per raster group. An XCD runs about CUs/8 tiles at once; with a
 // rows by b columns of them (a*b fixed) it fetches a*BM + b*BN/4 row-bytes of
 // X and W per K step (f16 X, 4-bit W), least near a = sqrt(CUs/8 * BN / (4 BM)).
@@ -886,7 +884,7 @@ int raster_group_m(int tiles_m, int bm, int bn) {
     const int v = std::atoi(e);
     if (v > 0) return std::min(v, tiles_m);
   }
-  const double conc = (double)std::max<int64_t>(1, num_cus() / 8);
+  const double conc = (double)std::max<int64_t>(1, device_cus() / 8);
   const double best = std::sqrt(conc * bn / (4.0 * bm));
   int a = 1;
   while (a * 2 <= tiles_m && a * 2 <= best * 1.41421356) a *= 2;
@@ -981,19 +979,6 @@ int env_int(const char* name, int dflt) {
   return e ? std::atoi(e) : dflt;
 }
 
-// Compute units of the current device (queried once per device).
-int64_t num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  check_hip(hipGetDevice(&dev), "hipGetDevice");
-  if (dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int v = 0;
-    check_hip(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    cached[dev] = v > 0 ? v : 256;
-  }
-  return cached[dev];
-}
 
 // Tile choice. f16/bf16 problems with K % 64 == 0 and group = 64 * 2^j use the
 // large-tile kernel with the largest tile that still yields a full wave of
@@ -1015,7 +1000,7 @@ void launch_mode(const GemmProblem& p) {
     // 256 x 256, e.g. 2048 x 14336 = 512 tiles (two full waves on 256 CUs)
     // instead of 448 (1.75).
     auto fill = [&](int64_t t) {
-      const int64_t cus = num_cus();
+      const int64_t cus = device_cus();
       return (double)t / (double)(((t + cus - 1) / cus) * cus);
     };
     if (tiles(256, 224) >= 240 && fill(tiles(256, 224)) > fill(tiles(256, 256)) + 0.05) cfg = 9;
@@ -1035,7 +1020,7 @@ void launch_mode(const GemmProblem& p) {
         // at M = 129..1024 on 4096..14336-deep, 1024..8192-wide problems
         // (e.g. 14336 -> 4096 at M = 256: 175 -> 70 us with 4 splits); odd
         // split counts and more than one workgroup per CU measured slower.
-        while (splits < 8 && t * splits * 2 <= num_cus() && stages / (splits * 2) >= 4) splits *= 2;
+        while (splits < 8 && t * splits * 2 <= device_cus() && stages / (splits * 2) >= 4) splits *= 2;
       }
     }
   }

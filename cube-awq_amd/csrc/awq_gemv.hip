@@ -817,9 +817,13 @@ void launch_mfma_cfg(const GemmProblem& p) {
 }
 
 // Small-M matrix-core path: 8 waves per workgroup, 64 rows per wave when the
-// group allows and that still gives >= 192 workgroups, else 32. (Fewer waves
-// per workgroup measured slower at every shape tried: more K splits cost
-// more in the final reduction than the extra workgroups gain.)
+// group allows and that still gives >= 192 workgroups, else 32. Also 32 for
+// 2..4 rows when 64 would already give two workgroups per CU: those
+// configurations hold two 8-wave workgroups per CU (<= 128 VGPRs), and the
+// second hides the first's loads (8192 -> 28672 at M = 2/4: 51/56 -> 39/45
+// us); with 8 rows the registers allow one, and the extra K splits only cost.
+// (Fewer waves per workgroup measured slower at every shape tried: more K
+// splits cost more in the final reduction than the extra workgroups gain.)
 template <int XT, int MV>
 void launch_mfma(const GemmProblem& p) {
   const int chunks = (int)((p.N / 8 + 63) / 64);
@@ -829,6 +833,7 @@ void launch_mfma(const GemmProblem& p) {
   int rpw = p.group % 64 == 0 ? 64 : 32;
   int waves = 8;
   if (rpw == 64 && wgs(8, 64) < 192) rpw = 32;
+  if (rpw == 64 && MV <= 4 && wgs(8, 64) >= 2 * device_cus()) rpw = 32;
   if (int v = env_int("AWQ_MFMA_WAVES", 0); v == 4 || v == 8) waves = v;
   if (int v = env_int("AWQ_MFMA_RPW", 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
   if (waves == 8 && rpw == 64) return launch_mfma_cfg<XT, MV, 8, 64>(p);

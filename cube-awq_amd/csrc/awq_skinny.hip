@@ -421,19 +421,6 @@ int env_int(const char* name, int dflt) {
   return e ? std::atoi(e) : dflt;
 }
 
-int64_t cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  check_hip(hipGetDevice(&dev), "hipGetDevice");
-  if (dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int v = 0;
-    check_hip(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    cached[dev] = v > 0 ? v : 256;
-  }
-  return cached[dev];
-}
-
 template <int MT>
 void launch_mt(const GemmProblem& p) {
   constexpr int kXSlot = 16 * MT * 64;
@@ -447,7 +434,7 @@ void launch_mt(const GemmProblem& p) {
   // chunk for the last workgroup to sum (splits x M): beyond those the split-K
   // traffic and the serial reduction cost more than the extra workgroups gain
   // (measured on 4096..14336-deep, 4096..28672-wide problems, 32..128 rows).
-  int splits = (int)std::max<int64_t>(1, cu_count() / chunks);
+  int splits = (int)std::max<int64_t>(1, device_cus() / chunks);
   splits = std::min(splits, std::max(1, total_steps / 16));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (8 * p.rows)));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, 1024 / p.rows));
