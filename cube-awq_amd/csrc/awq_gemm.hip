@@ -1010,17 +1010,36 @@ void launch_mode(const GemmProblem& p) {
       cfg = 4;  // 128 x 128 tiles, two workgroups per CU
       const int64_t t = tiles(128, 128);
       const int64_t stages = p.K / kBK;
+      // Fewer tiles than CUs: double the K splits while the workgroups still
+      // fit one per CU (at most 8, at least 4 stages each); odd split counts
+      // and more than one workgroup per CU measured slower.
+      auto pow2_splits = [&](int64_t tl) {
+        int sp = 1;
+        while (sp < 8 && tl * sp * 2 <= device_cus() && stages / (sp * 2) >= 4) sp *= 2;
+        return sp;
+      };
       if (p.rows <= 128) {
         // Skinny problems: split K across workgroups until ~320 are in
         // flight (at most 8 splits, at least 4 stages each).
         splits = (int)std::min<int64_t>({(320 + t - 1) / t, 8, std::max<int64_t>(stages / 4, 1)});
       } else {
-        // Fewer tiles than CUs: double the K splits while the workgroups
-        // still fit one per CU (at most 8, at least 4 stages each). Measured
-        // at M = 129..1024 on 4096..14336-deep, 1024..8192-wide problems
-        // (e.g. 14336 -> 4096 at M = 256: 175 -> 70 us with 4 splits); odd
-        // split counts and more than one workgroup per CU measured slower.
-        while (splits < 8 && t * splits * 2 <= device_cus() && stages / (splits * 2) >= 4) splits *= 2;
+        // 128 x 128 or 128 x 256 tiles, each with its split count. Time in
+        // units of one 128 x 128 x K tile: waves of workgroups over the CUs
+        // times the work of one (1/splits, or 2/splits for the wider tile).
+        // The wider tiles when that is no longer and they either need at most
+        // 4 splits or give each split >= 16 stages (8 splits of short K lose
+        // to the last workgroup's sum of 8 partial tiles). Measured at
+        // M = 129..768, K 4096..28672, N 1024..14336: e.g. 14336 -> 4096 at
+        // M = 256 175 -> 62 us, 28672 -> 8192 at M = 256 218 -> 180 us.
+        splits = pow2_splits(t);
+        const int64_t t3 = tiles(128, 256);
+        const int s3 = pow2_splits(t3);
+        const int64_t cus = device_cus();
+        const int64_t waves4 = (t * splits + cus - 1) / cus, waves3 = (t3 * s3 + cus - 1) / cus;
+        if (2 * waves3 * splits <= waves4 * s3 && (s3 <= 4 || stages / s3 >= 16)) {
+          cfg = 3;
+          splits = s3;
+        }
       }
     }
   }
