@@ -88,7 +88,6 @@ struct GemmArgs {
   int32_t splits, stages_per_split;
   float* partial;
   uint32_t* counters;
-  int32_t act;  // gate/up SiLU epilogue (store_out)
 };
 
 constexpr int kTileCtrStride = 64;  // u32 words between per-tile counters (256 B)
@@ -137,7 +136,10 @@ struct Tile {
 // Hint for the register allocator: the 256x256 tile runs one workgroup per CU.
 constexpr int min_blocks(int tile_elems) { return tile_elems >= 256 * 256 ? 1 : 2; }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ>
+// ACT: the gate/up SiLU epilogue (store_out). A template parameter, not a
+// kernel argument: as a runtime flag its epilogue code changed the register
+// allocation of the main loop and cost 2.5-6 % on every prefill GEMM.
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ, bool ACT>
 __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kernel(GemmArgs a) {
   using C = Tile<MODE, BM, BN, WGM, WGN>;
   typedef typename C::T T;
@@ -361,8 +363,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
       for (int r = 0; r < 16; ++r) {
         const int m = m0 + wm * C::kWTM + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const float v = acc[i][j][r] + bias;
-        const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
-        if (m < a.M) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
+        const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
+        if (m < a.M) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
       }
     }
   }
@@ -427,7 +429,7 @@ struct BigTile {
   static_assert(kWTM % MS == 0 && kWTN % MS == 0, "wave tile must be whole MFMA blocks");
 };
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool ACT>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   using S = typename Elem<ST>::type;
@@ -849,7 +851,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
           if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
         // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
 #pragma unroll
-        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, a.act, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
       }
     }
     if (tid == 0)
@@ -869,8 +871,8 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       for (int r = 0; r < kAccN; ++r) {
         const int m = out_row(i, r);
         const float v = acc[i][j][r] + bias;
-        const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
-        if (m < a.M) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
+        const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
+        if (m < a.M) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
       }
     }
   }
@@ -891,8 +893,8 @@ int raster_group_m(int tiles_m, int bm, int bn) {
   return a;
 }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ>
-void launch_big(const GemmProblem& p, int splits) {
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool ACT>
+void launch_big_act(const GemmProblem& p, int splits) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   GemmArgs a{};
   a.x = p.x;
@@ -904,7 +906,6 @@ void launch_big(const GemmProblem& p, int splits) {
   a.st = p.st;
   a.bt = p.bt;
   a.yt = p.yt;
-  a.act = p.act;
   a.M = (int32_t)p.rows;
   a.K = (int32_t)p.K;
   a.N = (int32_t)p.N;
@@ -928,18 +929,27 @@ void launch_big(const GemmProblem& p, int splits) {
   }
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kSmem),
               "hipFuncSetAttribute(gemm_big)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ>), dim3(tiles, a.splits),
+  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT>), dim3(tiles, a.splits),
                      dim3(C::kThreads), C::kSmem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ>
-void launch_cfg(const GemmProblem& p) {
+// The SiLU epilogue exists for the AutoAWQ order only (awq_gemm_silu_mul).
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ>
+void launch_big(const GemmProblem& p, int splits) {
+  if constexpr (!SEQ) {
+    if (p.act) return launch_big_act<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, true>(p, splits);
+  }
+  launch_big_act<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, false>(p, splits);
+}
+
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ, bool ACT>
+void launch_cfg_act(const GemmProblem& p) {
   using C = Tile<MODE, BM, BN, WGM, WGN>;
   GemmArgs a{};
   a.x = p.x;
@@ -951,7 +961,6 @@ void launch_cfg(const GemmProblem& p) {
   a.st = p.st;
   a.bt = p.bt;
   a.yt = p.yt;
-  a.act = p.act;
   a.M = (int32_t)p.rows;
   a.K = (int32_t)p.K;
   a.N = (int32_t)p.N;
@@ -964,14 +973,22 @@ void launch_cfg(const GemmProblem& p) {
   const size_t smem = C::kSmem;
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ, ACT>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
               "hipFuncSetAttribute(gemm)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ>), dim3(tiles), dim3(C::kThreads),
+  hipLaunchKernelGGL((gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ, ACT>), dim3(tiles), dim3(C::kThreads),
                      smem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
+}
+
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ>
+void launch_cfg(const GemmProblem& p) {
+  if constexpr (!SEQ) {
+    if (p.act) return launch_cfg_act<MODE, ST, BM, BN, WGM, WGN, SEQ, true>(p);
+  }
+  launch_cfg_act<MODE, ST, BM, BN, WGM, WGN, SEQ, false>(p);
 }
 
 int env_int(const char* name, int dflt) {

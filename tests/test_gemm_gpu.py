@@ -309,7 +309,7 @@ def test_repeated_calls_bit_identical(dev, M):
 
 
 @pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9])
-@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("x_dt", ["f16", "bf16"])
 def test_prefill_every_tile_configuration(dev, monkeypatch, tile, splits, x_dt):
     """Every prefill kernel configuration (tile shape, MFMA shape, split-K),
