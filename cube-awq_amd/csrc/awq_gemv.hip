@@ -56,7 +56,6 @@ struct GemvArgs {
   int32_t K, N, group;
   int32_t splits;
   int32_t seq;        // sequential nibble order (packed lane j = column j)
-  int32_t act;        // gate/up SiLU epilogue (store_out)
 };
 
 template <int XT>
@@ -144,7 +143,9 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-template <int XT, int MT, int WAVES, int RPW>
+// ACT (both decode kernels): the gate/up SiLU epilogue (store_out), a template
+// parameter so the plain kernels' code is untouched by it.
+template <int XT, int MT, int WAVES, int RPW, bool ACT>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
   constexpr int kChunkCols = 512;  // 64 lanes x 8 columns
   __shared__ float red[WAVES][MT][kChunkCols];
@@ -360,8 +361,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     const int n = col_base + c;
     float v = res[i];
     if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
-    const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
-    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
+    const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
+    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
   }
 }
 
@@ -428,7 +429,7 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t i, float (&v)[8])
   }
 }
 
-template <int XT, int MV, int WAVES, int RPW>
+template <int XT, int MV, int WAVES, int RPW, bool ACT>
 __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   constexpr int kChunkCols = 512;
   constexpr bool kLo = XT != AWQ_F16;
@@ -686,8 +687,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
     const int n = col_base + c;
     float v = res[i];
     if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
-    const float pv = a.act ? __shfl_xor(v, 1, 64) : 0.f;
-    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, a.act, m, n, a.N, v, pv);
+    const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
+    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
   }
 }
 
@@ -719,15 +720,18 @@ void launch_cfg(const GemmProblem& p) {
   a.group = (int32_t)p.group;
   a.splits = splits;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
-  a.act = p.act;
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MT * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
     a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
     a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
   }
-  hipLaunchKernelGGL((gemv_kernel<XT, MT, WAVES, RPW>), dim3(chunks, splits), dim3(64 * WAVES), 0,
-                     p.stream, a);
+  if (p.act)
+    hipLaunchKernelGGL((gemv_kernel<XT, MT, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES), 0,
+                       p.stream, a);
+  else
+    hipLaunchKernelGGL((gemv_kernel<XT, MT, WAVES, RPW, false>), dim3(chunks, splits), dim3(64 * WAVES), 0,
+                       p.stream, a);
   check_hip(hipGetLastError(), "gemv kernel launch");
 }
 
@@ -804,15 +808,18 @@ void launch_mfma_cfg(const GemmProblem& p) {
   a.group = (int32_t)p.group;
   a.splits = splits;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
-  a.act = p.act;
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
     a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
     a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
   }
-  hipLaunchKernelGGL((gemv_mfma_kernel<XT, MV, WAVES, RPW>), dim3(chunks, splits), dim3(64 * WAVES),
-                     0, p.stream, a);
+  if (p.act)
+    hipLaunchKernelGGL((gemv_mfma_kernel<XT, MV, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES),
+                       0, p.stream, a);
+  else
+    hipLaunchKernelGGL((gemv_mfma_kernel<XT, MV, WAVES, RPW, false>), dim3(chunks, splits), dim3(64 * WAVES),
+                       0, p.stream, a);
   check_hip(hipGetLastError(), "gemv mfma kernel launch");
 }
 

@@ -65,7 +65,6 @@ struct SkinnyArgs {
   int32_t M, K, N, group;
   int32_t splits, steps_per_split;
   int32_t seq;         // sequential nibble order
-  int32_t act;         // gate/up SiLU epilogue (store_out); AutoAWQ order only
 };
 
 constexpr int waitcnt_vm(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -83,7 +82,9 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* dst, uint32_t vof
 // read touches spread over all banks.
 __device__ __forceinline__ int xswz(int r) { return (r >> 2) & 3; }
 
-template <int MT>
+// ACT: the gate/up SiLU epilogue (store_out; AutoAWQ order only), a template
+// parameter so the plain kernel's code is untouched by it.
+template <int MT, bool ACT>
 __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   constexpr int kT = 2;                        // 16-column MFMA tiles per wave
   constexpr int kXRows = 16 * MT;
@@ -378,14 +379,14 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
           if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
         // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
 #pragma unroll
-        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, a.act, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
       }
     }
     if (tid == 0)
       __hip_atomic_store(&a.counters[chunk * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
-  if (a.act) {
+  if constexpr (ACT) {
     // AutoAWQ order: tiles 0 and 1 of a lane hold packed lanes q and q + 4 of
     // its pack, i.e. columns 2 q and 2 q + 1 -- a gate/up pair.
     const int n = nbase + colt[0];
@@ -467,7 +468,6 @@ void launch_mt(const GemmProblem& p) {
   a.splits = splits;
   a.steps_per_split = sps;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
-  a.act = p.act;
   if (splits > 1) {
     a.counters = static_cast<uint32_t*>(
         workspace_get(p.stream, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));
@@ -476,12 +476,18 @@ void launch_mt(const GemmProblem& p) {
   }
   static bool attr_set = false;
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT>, hipFuncAttributeMaxDynamicSharedMemorySize,
+    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)smem),
+              "hipFuncSetAttribute(skinny)");
+    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
                                   (int)smem),
               "hipFuncSetAttribute(skinny)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((skinny_kernel<MT>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+  if (p.act)
+    hipLaunchKernelGGL((skinny_kernel<MT, true>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+  else
+    hipLaunchKernelGGL((skinny_kernel<MT, false>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
   check_hip(hipGetLastError(), "skinny kernel launch");
 }
 
