@@ -13,9 +13,9 @@
 //    v_mfma_f32_16x16x32 blocks) and walks its K range in 64-row stages.
 //  * X goes global -> LDS directly (buffer_load_dwordx4 ... lds, no VGPR
 //    staging), two stages ahead in three LDS buffers when they fit. Each LDS
-//    row is 128 bytes of eight 16-byte granules at slot g ^ swz(row), which
-//    keeps both the MFMA operand reads and the dequantised-W writes free of
-//    bank conflicts without padding.
+//    row is 128 bytes of eight 16-byte granules at slot g ^ swz<MS>(row),
+//    which keeps both the MFMA operand reads and the dequantised-W writes
+//    free of bank conflicts without padding.
 //  * Packed W, zeros and scales of stage s+2 are loaded into registers while
 //    W of stage s+1 is dequantised between the MFMAs of stage s (scheduling
 //    groups interleave a few VALU ops after each MFMA) and written to LDS
@@ -378,10 +378,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
 // (BN/WGN) block of Y in 32 x 32 MFMA tiles.
 //
 // LDS rows are 128 bytes (64 k of one row of X or one column of W) made of
-// eight 16-byte granules; granule g of row r is stored in slot g ^ swz(r).
-// The swizzle makes the MFMA operand reads (32 consecutive rows, one granule)
-// and the dequantised-W writes (rows 8 apart, one granule) bank-conflict
-// free without padding.
+// eight 16-byte granules; granule g of row r is stored in slot g ^ swz<MS>(r).
+// The swizzle makes the MFMA operand reads and the dequantised-W writes (rows
+// 8 apart, one granule) bank-conflict free without padding.
 //
 // Software pipeline per 64-row stage s (buffers s & 1):
 //   issue LDS-direct X loads for s+1 and packed W / zeros / scales for s+2,
@@ -393,7 +392,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, min_blocks(BM * BN)) void gemm_kern
 constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | ((lgkm & 0xF) << 8);
 }
-__device__ __forceinline__ int swz(int row) { return (row ^ (row >> 3)) & 7; }
+// Two swizzles, chosen by the MFMA shape; each measured free of bank
+// conflicts (SQ_LDS_BANK_CONFLICT, gfx950) for its operand reads and for the
+// dequantised-W writes: 32x32x16 reads (32 rows x 2 granules per instruction)
+// with (r ^ (r >> 3)) & 7, 16x16x32 reads (16 rows x 4 granules) with
+// ((r >> 1) ^ (r >> 4)) & 7 -- the first costs 4 conflict cycles per
+// 16x16x32 operand read.
+template <int MS> __device__ __forceinline__ int swz(int row) {
+  if constexpr (MS == 16) return ((row >> 1) ^ (row >> 4)) & 7;
+  else return (row ^ (row >> 3)) & 7;
+}
+// Both are w_slot_base(wp) ^ w_slot_flip(c) on W column 8 wp + c (c < 8).
+template <int MS> __device__ __forceinline__ int w_slot_base(int wp) {
+  if constexpr (MS == 16) return ((wp & 1) << 2) ^ ((wp >> 1) & 7);
+  else return wp & 7;
+}
+template <int MS> __device__ __forceinline__ uint32_t w_slot_flip(int c) {
+  return MS == 16 ? (uint32_t)(c >> 1) : (uint32_t)c;
+}
 
 // 16 bytes per lane from a buffer straight into LDS: lane l's data lands at
 // dst + 16 l (dst is wave-uniform; it goes through M0).
@@ -475,7 +491,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   for (int i = 0; i < kXIns; ++i) {
     const int row = 8 * (wave + i * NW) + (lane >> 3);
     const int grow = min(m0 + row, a.M - 1);  // rows past M read row M-1; never stored
-    const int gran = (lane & 7) ^ swz(row);
+    const int gran = (lane & 7) ^ swz<MS>(row);
     xvoff[i] = (uint32_t)(grow * a.K + gran * 8) * 2u;
   }
 
@@ -494,9 +510,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   const uint32_t wvoff = (uint32_t)((wq * RW) * np + pack) * 4u;
   const uint32_t row_bytes = (uint32_t)np * 4u;
   // LDS byte offset (within a W buffer) of this thread's k-run in column 8 wp:
-  // swz(8 wp + c) = (c ^ wp) & 7, so column 8 wp + c uses this slot ^ c.
+  // column 8 wp + c uses this slot ^ w_slot_flip(c).
   const uint32_t wl0 = (uint32_t)(wp * 8 * C::kRowBytes) +
-                       (uint32_t)((((wq * RW) >> 3) ^ (wp & 7)) << 4) + (((wq * RW) & 7) ? 8u : 0u);
+                       (uint32_t)((((wq * RW) >> 3) ^ w_slot_base<MS>(wp)) << 4) + (((wq * RW) & 7) ? 8u : 0u);
 
   // Two register sets for packed W / zeros / scales, used alternately: one
   // being dequantised, the other in flight two stages ahead.
@@ -583,7 +599,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     }
     uint32_t off = wl0;
     asm volatile("" : "+v"(off));  // recompute per use: keeps 8 addresses out of the register file
-    unsigned char* dst = smem_raw + ((off ^ (uint32_t)(c << 4)) + (uint32_t)(C::kNA * C::kABytes + buf * C::kBBytes + c * C::kRowBytes));
+    unsigned char* dst = smem_raw + ((off ^ (w_slot_flip<MS>(c) << 4)) + (uint32_t)(C::kNA * C::kABytes + buf * C::kBBytes + c * C::kRowBytes));
     if constexpr (RW == 8)
       *reinterpret_cast<u32x4*>(dst) = u32x4{dq[0], dq[1], dq[2], dq[3]};
     else
@@ -606,12 +622,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 #pragma unroll
     for (int i = 0; i < C::kI; ++i) {
       const int row = wm * C::kWTM + 16 * i + l16;
-      a16[i] = (uint32_t)(row * C::kRowBytes + ((h4 ^ swz(row)) << 4));
+      a16[i] = (uint32_t)(row * C::kRowBytes + ((h4 ^ swz<MS>(row)) << 4));
     }
 #pragma unroll
     for (int j = 0; j < C::kJ; ++j) {
       const int col = wn * C::kWTN + 16 * j + l16;
-      b16[j] = (uint32_t)(C::kNA * C::kABytes + col * C::kRowBytes + ((h4 ^ swz(col)) << 4));
+      b16[j] = (uint32_t)(C::kNA * C::kABytes + col * C::kRowBytes + ((h4 ^ swz<MS>(col)) << 4));
     }
   }
   const int h = lane >> 5;  // which 8-k half of the 16-k MFMA slice
@@ -620,9 +636,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // the 32-row step as an immediate. k-slice kq flips slot bits 1-2 (kq << 5).
   const uint32_t lr = (uint32_t)(lane & 31);
   const uint32_t a_base = (uint32_t)((wm * C::kWTM) * C::kRowBytes) + lr * C::kRowBytes +
-                          (uint32_t)((h ^ swz((int)lr)) << 4);
+                          (uint32_t)((h ^ swz<MS>((int)lr)) << 4);
   const uint32_t b_base = (uint32_t)(C::kNA * C::kABytes) + (uint32_t)((wn * C::kWTN) * C::kRowBytes) +
-                          lr * C::kRowBytes + (uint32_t)((h ^ swz((int)lr)) << 4);
+                          lr * C::kRowBytes + (uint32_t)((h ^ swz<MS>((int)lr)) << 4);
   const uint32_t a_fl = (uint32_t)(((wm * (C::kWTM / 8)) & 4) << 4);
   const uint32_t b_fl = (uint32_t)(((wn * (C::kWTN / 8)) & 4) << 4);
   const uint32_t a_par[2] = {a_base ^ a_fl, a_base ^ a_fl ^ 64u};
