@@ -108,3 +108,36 @@ def test_fused_projections_reject_mismatched_k_or_group():
     d.update(_proj("p2", 128, 64, 64, 30, bias=False))
     with pytest.raises(Panic, match="share d_input and group_size"):
         checkpoint.load_fused_awq_gemm_linear(d, ["p0", "p2"])
+
+
+def test_gate_up_silu_interleaves_columns():
+    """load_awq_gate_up_silu: column 2j of every tensor is gate column j and
+    2j + 1 up column j (qweight/qzeros as logical nibbles in AutoAWQ order)."""
+    from cube_awq import AWQGateUpSiLU, pack
+    m = "model.layers.0.mlp"
+    d = {}
+    d.update(_proj(f"{m}.gate_proj", 256, 96, 64, 40, bias=True))
+    d.update(_proj(f"{m}.up_proj", 256, 96, 64, 50, bias=False))
+    layer = checkpoint.load_awq_gate_up_silu(d, f"{m}.gate_proj", f"{m}.up_proj")
+    assert isinstance(layer, AWQGateUpSiLU) and layer.group_size() == 64
+    assert tuple(layer.qweight.shape) == (256, 24) and tuple(layer.scales.shape) == (4, 192)
+    for name in ("qweight", "qzeros"):
+        got = pack.unpack(layer.__dict__[name].numpy().view(np.uint32), "awq")
+        g = pack.unpack(d[f"{m}.gate_proj.{name}"].numpy().view(np.uint32), "awq")
+        u = pack.unpack(d[f"{m}.up_proj.{name}"].numpy().view(np.uint32), "awq")
+        assert np.array_equal(got[:, 0::2], g) and np.array_equal(got[:, 1::2], u), name
+    assert torch.equal(layer.scales[:, 0::2], d[f"{m}.gate_proj.scales"])
+    assert torch.equal(layer.scales[:, 1::2], d[f"{m}.up_proj.scales"])
+    assert torch.equal(layer.bias[0::2], d[f"{m}.gate_proj.bias"])
+    assert not layer.bias[1::2].any()
+
+
+def test_gate_up_silu_rejects_mismatched_projections():
+    d = {}
+    d.update(_proj("g", 256, 32, 64, 40, bias=False))
+    d.update(_proj("u", 256, 32, 64, 50, bias=False))
+    layer = checkpoint.load_awq_gate_up_silu(d, "g", "u")  # 2 x 32 = 64 interleaved: accepted
+    assert tuple(layer.scales.shape) == (4, 64)
+    d.update(_proj("u2", 256, 64, 64, 60, bias=False))
+    with pytest.raises(Panic, match="same shapes"):
+        checkpoint.load_awq_gate_up_silu(d, "g", "u2")
