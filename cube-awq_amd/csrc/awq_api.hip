@@ -152,7 +152,8 @@ static void check_float_dtype(int32_t t, const char* what) {
   if (!is_float_dtype(t)) panic(std::string(what) + " must have f32/f16/bf16 dtype");
 }
 
-// Run the GEMM over validated sizes: rows = m_valid, M <= 8 -> GEMV.
+// Run the GEMM over validated sizes: rows = m_valid; M <= 8 (and 9..16 when
+// the matrix-core decode kernel takes them) -> GEMV, else the prefill kernels.
 static void run_gemm(GemmProblem p, int64_t launch_m) {
   check_aligned(p.x, "input");
   check_aligned(p.qweight, "qweight");

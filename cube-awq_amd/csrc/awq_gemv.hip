@@ -1,4 +1,5 @@
-// awq_gemv.hip -- decode path (M <= 8) of the fused AWQ dequant-GEMM for gfx950.
+// awq_gemv.hip -- decode path (M <= 8, and 9..16 rows on the matrix cores) of
+// the fused AWQ dequant-GEMM for gfx950.
 //
 // y[m, n] = sum_k x[m, k] * (q[k, n] - z[k/g, n]) * s[k/g, n]   (AutoAWQ nibble order)
 // The reference's gemm_awq_decode (src/kernel/awq_kernel_gemm.rs:445-624) runs

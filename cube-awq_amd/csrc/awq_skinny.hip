@@ -7,15 +7,15 @@
 //
 // With few activation rows the large-tile kernel (awq_gemm.hip) is latency
 // bound: every 64-row stage of a 128..256-column tile is a load, dequantise,
-// barrier, MFMA round trip, and split-K partials of M x N floats cost as much
-// traffic as the weights. Here the weights stream as in the decode kernels:
+// barrier, MFMA round trip, and on wide outputs its tiles already fill the
+// CUs, so K splits cannot hide that. Here the weights stream as in the decode
+// kernels:
 //  * A workgroup owns 256 columns (32 packed words = 128 bytes of each row)
 //    and a run of K; 32-row steps of W, the matching 32 columns of X and,
 //    up front, the zeros and scales of the run's groups go global -> LDS
 //    directly (buffer_load ... lds, 16 bytes per lane for W and X, 4 for the
-//    zeros and scales) into a ring of kRing
-//    steps, kRing - 1 steps ahead, with explicit vmcnt waits and one
-//    s_barrier per step.
+//    zeros and scales) into a ring of kRing steps, kRing - 2 steps ahead,
+//    with explicit vmcnt waits and one s_barrier per two steps.
 //  * 8 waves: wave w takes packs 4 w .. 4 w + 3 (32 columns, two 16-column
 //    MFMA tiles) for every 16-row tile, so each weight is dequantised once.
 //    Lane (lg = lane / 16, lj = lane % 16) reads the 8 words of rows
