@@ -766,6 +766,11 @@ void launch_rpw(const GemmProblem& p) {
     return r;
   };
   while (waves > 4 && wgs(waves, cap(waves, rpw)) < 192) waves >>= 1;
+  // One row on small matrices: 8 waves of 32 rows even below 192 workgroups.
+  // Four waves (twice the workgroups and K splits) measured 18-34 % slower at
+  // 4096 x 4096, 4096 x 1024 and 8192 x 1024 (8.35 / 7.96 / 11.2 us against
+  // 6.86 / 6.54 / 7.57), sixteen 7-10 % slower.
+  if (MT == 1 && waves < 8 && WMAX >= 8 && rpw >= 32) waves = 8;
   rpw = cap(waves, rpw);
   // Long runs per wave (fewer splits) while the workgroup count stays high.
   while (rpw < 128 && 2 * rpw <= rpw_max(XT, MT, waves) && g % (2 * rpw) == 0 &&
