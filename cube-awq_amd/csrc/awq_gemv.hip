@@ -766,11 +766,13 @@ void launch_rpw(const GemmProblem& p) {
     return r;
   };
   while (waves > 4 && wgs(waves, cap(waves, rpw)) < 192) waves >>= 1;
-  // One row on small matrices: 8 waves of 32 rows even below 192 workgroups.
-  // Four waves (twice the workgroups and K splits) measured 18-34 % slower at
-  // 4096 x 4096, 4096 x 1024 and 8192 x 1024 (8.35 / 7.96 / 11.2 us against
-  // 6.86 / 6.54 / 7.57), sixteen 7-10 % slower.
+  // Small matrices keep more waves even below 192 workgroups: one row 8 waves
+  // of 32 rows (4 waves and twice the K splits measured 18-34 % slower at
+  // 4096 x 4096, 4096 x 1024 and 8192 x 1024: 8.35 / 7.96 / 11.2 us against
+  // 6.86 / 6.54 / 7.57; 16 waves 7-10 % slower), two rows 16 waves of 8
+  // (4096 x 1024: 12.8 us with 4 waves, 8.4 with 16).
   if (MT == 1 && waves < 8 && WMAX >= 8 && rpw >= 32) waves = 8;
+  if (MT == 2) waves = WMAX;
   rpw = cap(waves, rpw);
   // Long runs per wave (fewer splits) while the workgroup count stays high.
   while (rpw < 128 && 2 * rpw <= rpw_max(XT, MT, waves) && g % (2 * rpw) == 0 &&
@@ -858,11 +860,12 @@ void launch_mfma(const GemmProblem& p) {
 template <int XT>
 void launch_xt(const GemmProblem& p) {
   // 2..8 rows: matrix cores, whose cost per weight does not grow with M,
-  // except 2 rows of a small, wide matrix (K x N <= 4096 x 4096, N >= 4096),
-  // where the VALU kernel measured faster (AWQ_DECODE_MFMA=0/1 forces the
-  // choice).
+  // except 2 rows of a small matrix (K x N <= 4096 x 4096), where the VALU
+  // kernel with 16 waves measured faster (4096 x 4096 / 4096 x 1024 /
+  // 8192 x 1024: 8.4 / 8.4 / 10.3 us against 10.5 / 10.2 / 11.7).
+  // AWQ_DECODE_MFMA=0/1 forces the choice.
   const int force = env_int("AWQ_DECODE_MFMA", -1);
-  const bool small2 = p.rows == 2 && p.K * p.N <= 4096ll * 4096ll && p.N >= 4096;
+  const bool small2 = p.rows == 2 && p.K * p.N <= 4096ll * 4096ll;
   const bool mfma_ok = p.rows >= 2 && p.group % 32 == 0 && p.K % 32 == 0 &&
                        (force == 1 || (force != 0 && !small2));
   if (p.rows > 8) return launch_mfma<XT, 16>(p);  // accepted by small_m_mfma_ok
