@@ -1,9 +1,10 @@
 // awq_skinny.hip -- fused AWQ dequant-GEMM for skinny problems (17..128 rows,
-// f16 activations) on gfx950.
+// f16 or bf16 activations) on gfx950.
 //
-// Y[M, N] = X[M, K] . W[K, N], W[k, n] = f16((q - z) * s), the reference's
-// F = f16 dequantised weight (gemm_awq, src/kernel/awq_kernel_gemm.rs:181-439),
-// accumulated in fp32 on v_mfma_f32_16x16x32_f16.
+// Y[M, N] = X[M, K] . W[K, N], W[k, n] = F((q - z) * s) for F = f16 or bf16,
+// the reference's F-typed dequantised weight (gemm_awq,
+// src/kernel/awq_kernel_gemm.rs:181-439), accumulated in fp32 on
+// v_mfma_f32_16x16x32_f16 / _bf16.
 //
 // With few activation rows the large-tile kernel (awq_gemm.hip) is latency
 // bound: every 64-row stage of a 128..256-column tile is a load, dequantise,
@@ -23,7 +24,12 @@
 //    of tile t from packed lane c = 4 t + (lj >> 2): one v_perm_b32 gathers
 //    byte c / 2 of two rows, one v_bitop3_b32 makes the f16 magic 1024 + q
 //    (64 + q for the high nibble), then an exact v_pk_add_f16 of -(1024 + z)
-//    and one v_pk_mul_f16 by s: 2 VALU ops per weight.
+//    and one v_pk_mul_f16 by s: 2 VALU ops per weight. bf16 (no packed bf16
+//    arithmetic on gfx950): after the same v_perm_b32, one v_and_b32 leaves
+//    q (or 16 q) in bytes 0 and 2, v_cvt_f32_ubyte0/2 convert them, one
+//    v_fma_f32 per weight forms q s' - z s = (q - z) s exactly (s' = s or
+//    s / 16; exact for 16-bit scales), and v_cvt_pk_bf16_f32 rounds each pair
+//    once: 3.5 VALU ops per weight.
 //  * Waves never share outputs, so there is no cross-wave reduction; K
 //    splits (grid.y) publish fp32 partials and the last workgroup to arrive on
 //    a chunk sums them in split order (deterministic), adds the bias and
@@ -32,6 +38,7 @@
 // M*K*2 + M*N*sizeof(y).
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "awq_common.h"
 
@@ -39,6 +46,7 @@ namespace cube_awq {
 namespace {
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
@@ -83,9 +91,11 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* dst, uint32_t vof
 __device__ __forceinline__ int xswz(int r) { return (r >> 2) & 3; }
 
 // ACT: the gate/up SiLU epilogue (store_out; AutoAWQ order only), a template
-// parameter so the plain kernel's code is untouched by it.
-template <int MT, bool ACT>
+// parameter so the plain kernel's code is untouched by it. BF: bf16
+// activations (16-bit scales), W dequantised through f32 (see compute).
+template <int MT, bool ACT, bool BF>
 __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
+  typedef typename std::conditional<BF, bf16x8_t, f16x8_t>::type XV;
   constexpr int kT = 2;                        // 16-column MFMA tiles per wave
   constexpr int kXRows = 16 * MT;
   constexpr int kXSlot = kXRows * 64;          // 32 f16 columns of X per row
@@ -198,6 +208,7 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     for (int t = 0; t < kT; ++t) acc[i][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   f16x2_t fz[kT], fs[kT];
+  float bs[kT], bzs[kT];  // BF: s (s / 16 for the high nibble) and -z s
   // Group of the loaded zeros and scales, counted per step instead of divided
   // out: the run starts g_skip steps into group g_first.
   const int g_steps = a.group / kStep;
@@ -206,7 +217,7 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
 
   // LDS -> registers for one step: the 8 W words of this lane's pack and the
   // A operands of every row tile.
-  auto fetch = [&](int s, uint32_t (&wv)[8], f16x8_t (&av)[MT]) {
+  auto fetch = [&](int s, uint32_t (&wv)[8], XV (&av)[MT]) {
     const unsigned char* wsl = wring + (s % kRing) * kWSlot;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -217,13 +228,13 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
       const int r = 16 * i + lj;
-      av[i] = *reinterpret_cast<const f16x8_t*>(xsl + r * 64 + ((lg ^ xswz(r)) << 4));
+      av[i] = *reinterpret_cast<const XV*>(xsl + r * 64 + ((lg ^ xswz(r)) << 4));
     }
   };
 
   // One step (steps are computed in order): the zero points and scales when
   // a group starts, then 2 B operands and 2 MT MFMAs.
-  auto compute = [&](const uint32_t (&wv)[8], const f16x8_t (&av)[MT]) {
+  auto compute = [&](const uint32_t (&wv)[8], const XV (&av)[MT]) {
     if (g_left == 0) {
       ++cur_g;
       g_left = cur_g == 0 ? g_steps - g_skip : g_steps;
@@ -232,31 +243,50 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int t = 0; t < kT; ++t) {
         const uint32_t zh = __builtin_amdgcn_perm(zw, zw, selt[t]);
-        fz[t] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(zh, hmask, hexp, 0xEA));
         const int col = 8 * pl + colt[t];
         float sv;
         if (es == 4) sv = reinterpret_cast<const float*>(slds + g * kCols * 4)[col];
         else if (a.st == AWQ_F16) sv = (float)reinterpret_cast<const f16_t*>(slds + g * kCols * 4)[col];
         else sv = to_f32(reinterpret_cast<const bf16_t*>(slds + g * kCols * 4)[col]);
-        const _Float16 sh = (_Float16)sv;
-        fs[t] = f16x2_t{sh, sh};
+        if constexpr (BF) {
+          // z s is exact in f32 for 16-bit scales (4 by at most 11 bits).
+          const int z = (int)((zh >> (4 * hh)) & 0xFu);
+          bs[t] = hh ? sv * 0.0625f : sv;
+          bzs[t] = -(float)z * sv;
+        } else {
+          fz[t] = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(zh, hmask, hexp, 0xEA));
+          const _Float16 sh = (_Float16)sv;
+          fs[t] = f16x2_t{sh, sh};
+        }
       }
     }
     --g_left;
 #pragma unroll
     for (int t = 0; t < kT; ++t) {
-      f16x8_t bq;
+      XV bq;
 #pragma unroll
       for (int u = 0; u < 8; u += 2) {
         const uint32_t h = __builtin_amdgcn_perm(wv[u + 1], wv[u], selt[t]);
-        const f16x2_t v = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(h, hmask, hexp, 0xEA));
-        const f16x2_t d = (v - fz[t]) * fs[t];
-        bq[u] = d[0];
-        bq[u + 1] = d[1];
+        if constexpr (BF) {
+          // Bytes 0 and 2 hold q (or 16 q): v_cvt_f32_ubyte0/2, then one fma
+          // gives (q - z) s exactly (q s and z s are exact, so is their
+          // difference), rounded once to bf16 (v_cvt_pk_bf16_f32).
+          const uint32_t hm = h & hmask;
+          const float q0 = (float)(hm & 0xFFu), q1 = (float)((hm >> 16) & 0xFFu);
+          bq[u] = (__bf16)__builtin_fmaf(q0, bs[t], bzs[t]);
+          bq[u + 1] = (__bf16)__builtin_fmaf(q1, bs[t], bzs[t]);
+        } else {
+          const f16x2_t v = __builtin_bit_cast(f16x2_t, __builtin_amdgcn_bitop3_b32(h, hmask, hexp, 0xEA));
+          const f16x2_t d = (v - fz[t]) * fs[t];
+          bq[u] = d[0];
+          bq[u + 1] = d[1];
+        }
       }
 #pragma unroll
-      for (int i = 0; i < MT; ++i)
-        acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bq, acc[i][t], 0, 0, 0);
+      for (int i = 0; i < MT; ++i) {
+        if constexpr (BF) acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bq, acc[i][t], 0, 0, 0);
+        else acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av[i], bq, acc[i][t], 0, 0, 0);
+      }
     }
   };
 
@@ -277,7 +307,7 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     if (s + kRing - 2 < steps) issue(s + kRing - 2);
     if (s + kRing - 1 < steps) issue(s + kRing - 1);
     uint32_t wa[8], wb[8];
-    f16x8_t xa[MT], xb[MT];
+    XV xa[MT], xb[MT];
     const bool two = s + 1 < steps;
     if constexpr (MT <= 3) {
       fetch(s, wa, xa);
@@ -422,7 +452,7 @@ int env_int(const char* name, int dflt) {
   return e ? std::atoi(e) : dflt;
 }
 
-template <int MT>
+template <int MT, bool BF>
 void launch_mt(const GemmProblem& p) {
   constexpr int kXSlot = 16 * MT * 64;
   const size_t smem = (size_t)kRing * kWSlot + (size_t)kRing * kXSlot + (size_t)kMaxGroups * kPacks * 4 +
@@ -476,19 +506,28 @@ void launch_mt(const GemmProblem& p) {
   }
   static bool attr_set = false;
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)smem),
+    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, false, BF>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
               "hipFuncSetAttribute(skinny)");
-    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)smem),
+    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, true, BF>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
               "hipFuncSetAttribute(skinny)");
     attr_set = true;
   }
   if (p.act)
-    hipLaunchKernelGGL((skinny_kernel<MT, true>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+    hipLaunchKernelGGL((skinny_kernel<MT, true, BF>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
   else
-    hipLaunchKernelGGL((skinny_kernel<MT, false>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+    hipLaunchKernelGGL((skinny_kernel<MT, false, BF>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
   check_hip(hipGetLastError(), "skinny kernel launch");
+}
+
+template <bool BF>
+void launch_rows(const GemmProblem& p) {
+  if (p.rows <= 32) return launch_mt<2, BF>(p);
+  if (p.rows <= 48) return launch_mt<3, BF>(p);
+  if (p.rows <= 64) return launch_mt<4, BF>(p);
+  if (p.rows <= 96) return launch_mt<6, BF>(p);
+  return launch_mt<8, BF>(p);
 }
 
 }  // namespace
@@ -502,17 +541,16 @@ bool skinny_ok(const GemmProblem& p) {
   const int force = env_int("AWQ_SKINNY", -1);
   const bool wins = p.N >= 6144 || (p.N >= 1024 && (p.rows <= 32 || (p.rows <= 64 && p.K >= 8192)));
   if (force == 0 || (force != 1 && !wins)) return false;
-  return p.xt == AWQ_F16 && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
+  // bf16 activations need 16-bit scales (z s exact in f32, see the kernel).
+  const bool types = p.xt == AWQ_F16 || (p.xt == AWQ_BF16 && p.st != AWQ_F32);
+  return types && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
          p.N % 32 == 0 && p.K * (p.N / 8) * 4 < (1ll << 32) && p.rows * p.K * 2 < (1ll << 32) &&
          (p.K / p.group) * p.N * 4 < (1ll << 32);
 }
 
 void launch_skinny(const GemmProblem& p) {
-  if (p.rows <= 32) return launch_mt<2>(p);
-  if (p.rows <= 48) return launch_mt<3>(p);
-  if (p.rows <= 64) return launch_mt<4>(p);
-  if (p.rows <= 96) return launch_mt<6>(p);
-  return launch_mt<8>(p);
+  if (p.xt == AWQ_BF16) return launch_rows<true>(p);
+  launch_rows<false>(p);
 }
 
 }  // namespace cube_awq

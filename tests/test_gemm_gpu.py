@@ -14,7 +14,7 @@ import awq_oracle as oracle
 import cube_awq
 from cube_awq import AWQGEMMLinear, ShapeConfig, _lib, synth
 from conftest import load_golden
-from helpers import TORCH_OF, host_f32, make_problem, to_device, to_host
+from helpers import TORCH_OF, host_f32, make_problem, round_to, to_device, to_host
 
 pytestmark = pytest.mark.gpu
 
@@ -404,23 +404,50 @@ def test_small_m_every_configuration(dev, monkeypatch, rpw):
     assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, None, g, "f32", "f32")) <= TOL_FP32
 
 
-# 17..128 rows of f16 activations run on the skinny kernel (awq_skinny.hip);
-# AWQ_SKINNY=0 sends them to the large-tile kernels.
+# 17..128 rows of f16 or bf16 activations (16-bit scales) run on the skinny
+# kernel (awq_skinny.hip); AWQ_SKINNY=0 sends them to the large-tile kernels.
 @pytest.mark.parametrize("path", ["1", "0"])
 @pytest.mark.parametrize("M", [17, 33, 48, 64, 80, 96, 100, 128])
-def test_skinny_both_paths(dev, monkeypatch, path, M):
+@pytest.mark.parametrize("x_dt", ["f16", "bf16"])
+def test_skinny_both_paths(dev, monkeypatch, path, M, x_dt):
     monkeypatch.setenv("AWQ_SKINNY", path)
     K, N, g = 2048, 2080, 128  # N % 256 != 0: ragged last chunk
-    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt="f16", bias=True)
-    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f16", "f16", "f32")
-    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, "f16", "f16")) <= TOL_MFMA
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=x_dt, bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, x_dt, "f32")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, x_dt, x_dt)) <= TOL_MFMA
 
 
 @pytest.mark.parametrize("splits", [1, 3, 8, 64])
-@pytest.mark.parametrize("s_dt,g", [("f16", 64), ("f32", 128), ("bf16", 256)])
-def test_skinny_every_split(dev, monkeypatch, splits, s_dt, g):
+@pytest.mark.parametrize("x_dt,s_dt,g", [("f16", "f16", 64), ("f16", "f32", 128), ("f16", "bf16", 256),
+                                         ("bf16", "bf16", 64), ("bf16", "f16", 128)])
+def test_skinny_every_split(dev, monkeypatch, splits, x_dt, s_dt, g):
     monkeypatch.setenv("AWQ_SKINNY_SPLITS", str(splits))
     M, K, N = 48, 4096, 768
-    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt=s_dt, bias=True)
-    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f16", s_dt, "f16"))
-    assert oracle.rel_l2(host_f32(y, "f16"), _ref64(x, qw, qz, sc, b, g, "f16", s_dt)) <= TOL_MFMA
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
+    # bf16 output would add a rounding of relative size ~2^-9 to the bf16
+    # weights' own; f16 output is also covered here.
+    y_dt = "f16" if x_dt == "f16" else "f32"
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, y_dt))
+    assert oracle.rel_l2(host_f32(y, y_dt), _ref64(x, qw, qz, sc, b, g, x_dt, s_dt)) <= TOL_MFMA
+
+
+@pytest.mark.parametrize("M", [48, 128])
+@pytest.mark.parametrize("splits", ["1", "3"])
+@pytest.mark.parametrize("x_dt,s_dt", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f16"), ("f16", "bf16")])
+def test_skinny_weights_exact(dev, monkeypatch, M, splits, x_dt, s_dt):
+    """Each row of X selects one k (a single 1), so row m of Y is row k_m of
+    the weights as the kernel dequantised them, with nothing else added:
+    bit-exact against (q - z) * s rounded once to the activation type (the
+    reference's F-typed dequant, src/kernel/awq_kernel_gemm.rs:181-439)."""
+    monkeypatch.setenv("AWQ_SKINNY", "1")
+    monkeypatch.setenv("AWQ_SKINNY_SPLITS", splits)
+    K, N, g = 2048, 768, 128
+    _, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt)
+    ks = (np.arange(M) * 37 + 5) % K  # distinct rows, in every split's range
+    x32 = np.zeros((M, K), dtype=np.float32)
+    x32[np.arange(M), ks] = 1.0
+    x = round_to(x32, x_dt)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, x_dt, s_dt, "f32"))
+    w32 = oracle.dequant(qw, qz, host_f32(sc, s_dt), g, order="awq")  # exact for 16-bit scales
+    want = host_f32(round_to(w32[ks], x_dt), x_dt)
+    assert np.array_equal(y, want)

@@ -75,16 +75,17 @@ def test_sequential_every_tile_configuration(dev, monkeypatch, tile, dt):
 
 
 @pytest.mark.parametrize("M", [17, 64, 128])
-def test_sequential_skinny_kernel(dev, monkeypatch, M):
-    """17..128 rows of f16 on the skinny kernel, forced on at a narrow N."""
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_sequential_skinny_kernel(dev, monkeypatch, M, dt):
+    """17..128 rows of f16 or bf16 on the skinny kernel, forced on at a narrow N."""
     monkeypatch.setenv("AWQ_SKINNY", "1")
     K, N, g = 2048, 2080, 128
-    x, qw_awq, qz_awq, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt="f16", bias=True)
+    x, qw_awq, qz_awq, sc, b = make_problem(M, K, N, g, x_dt=dt, s_dt=dt, bias=True)
     qw_seq, qz_seq = _to_seq(qw_awq), _to_seq(qz_awq)
-    y_seq = _run(dev, x, qw_seq, qz_seq, sc, b, M, K, N, g, "f16", _lib.AWQ_ORDER_SEQUENTIAL, "f32")
-    y_awq = _run(dev, x, qw_awq, qz_awq, sc, b, M, K, N, g, "f16", _lib.AWQ_ORDER_AUTOAWQ, "f32")
+    y_seq = _run(dev, x, qw_seq, qz_seq, sc, b, M, K, N, g, dt, _lib.AWQ_ORDER_SEQUENTIAL, "f32")
+    y_awq = _run(dev, x, qw_awq, qz_awq, sc, b, M, K, N, g, dt, _lib.AWQ_ORDER_AUTOAWQ, "f32")
     assert np.array_equal(y_seq.view(np.uint32), y_awq.view(np.uint32))
-    ref = oracle.gemm_f64(host_f32(x, "f16"), qw_seq, qz_seq, host_f32(sc, "f16"), g, bias=b, order="seq")
+    ref = oracle.gemm_f64(host_f32(x, dt), qw_seq, qz_seq, host_f32(sc, dt), g, bias=b, order="seq")
     assert oracle.rel_l2(y_seq, ref) <= TOL_MFMA
 
 

@@ -59,6 +59,8 @@ ROUTES = [
     (17, "f16", {}),                                  # skinny, split-K
     (64, "f16", {"AWQ_SKINNY_SPLITS": "1"}),          # skinny, direct store
     (100, "f16", {}),
+    (24, "bf16", {}),                                 # skinny bf16, split-K
+    (96, "bf16", {"AWQ_SKINNY": "1", "AWQ_SKINNY_SPLITS": "1"}),  # skinny bf16, direct store
     (64, "f16", {"AWQ_SKINNY": "0"}),                 # large tiles, split-K
     (300, "f16", {}),                                 # large tiles, direct store
     (300, "bf16", {}),
