@@ -586,12 +586,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       // significand); one rounding to bf16 gives the bf16 product.
       const int z = (int)((zw >> (4 * L)) & 0xFu);
       const float sv_ = scale_of(r_.sv, c);
+      // 16-bit scales: z s is exact, so fma(q, s, -z s) is (q - z) s exactly
+      // in one op after the conversion of q (v_bfe_u32, v_cvt_f32_ubyte0,
+      // v_fma_f32). f32 scales: (q - z) converted, then multiplied.
+      const float nzs = -(float)z * sv_;
 #pragma unroll
       for (int r = 0; r < RW / 2; ++r) {
-        const int q0 = (int)((r_.w[2 * r] >> (4 * L)) & 0xFu);
-        const int q1 = (int)((r_.w[2 * r + 1] >> (4 * L)) & 0xFu);
-        const bf16_t v0 = from_f32<bf16_t>((float)(q0 - z) * sv_);
-        const bf16_t v1 = from_f32<bf16_t>((float)(q1 - z) * sv_);
+        const uint32_t q0 = (r_.w[2 * r] >> (4 * L)) & 0xFu;
+        const uint32_t q1 = (r_.w[2 * r + 1] >> (4 * L)) & 0xFu;
+        float d0, d1;
+        if constexpr (sizeof(S) == 4) {
+          d0 = (float)((int)q0 - z) * sv_;
+          d1 = (float)((int)q1 - z) * sv_;
+        } else {
+          d0 = __builtin_fmaf((float)q0, sv_, nzs);
+          d1 = __builtin_fmaf((float)q1, sv_, nzs);
+        }
+        const bf16_t v0 = from_f32<bf16_t>(d0);
+        const bf16_t v1 = from_f32<bf16_t>(d1);
         dq[r] = (uint32_t)__builtin_bit_cast(uint16_t, v0) | ((uint32_t)__builtin_bit_cast(uint16_t, v1) << 16);
       }
     }
@@ -1074,6 +1086,36 @@ void launch_mode(const GemmProblem& p) {
           cfg = 3;
           splits = s3;
         }
+      }
+    }
+    // 257..1024 rows with too few 256-row tiles for the first two rules: a
+    // cost model fitted to a sweep of M 384..1024, K 4096..28672, N
+    // 4096..28672 (tiles 256x224, 256x256, 128x256; 1 or 2 K splits). Time =
+    // waves of workgroups (one per CU) x stages per split x per-stage time
+    // (1.9 / 2.1 / 1.2 us), plus for K splits the partials' round trip
+    // (splits x M x N x 8 bytes at 4 TB/s, + 10 us). The 256-row tiles
+    // replace the choice above only when the model puts them 10 % ahead of
+    // the best 128 x 256 option: e.g. 4096 -> 14336 at M = 768 169 -> 136 us,
+    // 28672 -> 8192 at M = 768 516 -> 451 us; no swept point got slower.
+    if (p.rows > 256 && p.rows <= 1024 && p.N >= 4096 && tiles(256, 224) < 240) {
+      const int64_t cus = device_cus();
+      const int64_t stages = p.K / kBK;
+      auto est = [&](int bm, int bn, int sp, double per_stage) {
+        const int64_t waves = (tiles(bm, bn) * sp + cus - 1) / cus;
+        const int64_t st = (stages + sp - 1) / sp;
+        const double partials = sp > 1 ? (double)sp * (double)p.rows * (double)p.N * 8.0 / 4e6 + 10.0 : 0.0;
+        return (double)(waves * st) * per_stage + partials;
+      };
+      struct Cand { int cfg, sp; double t; };
+      const Cand big[4] = {{9, 1, est(256, 224, 1, 1.9)}, {9, 2, est(256, 224, 2, 1.9)},
+                           {2, 1, est(256, 256, 1, 2.1)}, {2, 2, est(256, 256, 2, 2.1)}};
+      Cand b = big[0];
+      for (const Cand& c : big)
+        if (c.t < b.t) b = c;
+      const double mid = std::min(est(128, 256, 1, 1.2), est(128, 256, 2, 1.2));
+      if (b.t < 0.9 * mid) {
+        cfg = b.cfg;
+        splits = b.sp;
       }
     }
   }

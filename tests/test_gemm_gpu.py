@@ -214,6 +214,20 @@ def test_prefill_m2048_gate_up_sampled_rows(dev):
     assert oracle.rel_l2(got, _ref64(x[rows], qw, qz, sc, None, g, "f16", "f16")) <= TOL_MFMA
 
 
+@pytest.mark.parametrize("M,K,N,x_dt", [(768, 4096, 14336, "f16"), (768, 28672, 8192, "f16"),
+                                         (768, 4096, 14336, "bf16"), (300, 4096, 14336, "f16"),
+                                         (1024, 28672, 8192, "f16")])
+def test_prefill_mid_range_routes_sampled_rows(dev, M, K, N, x_dt):
+    # 257..1024 rows with few 256-row tiles: the launcher's default choice
+    # (256 x 224 tiles, with 2 K splits at 28672 -> 8192 and M = 768),
+    # checked on 24 sampled rows including the last.
+    g = 128
+    x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt=x_dt, s_dt=x_dt)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, x_dt, x_dt, "f32"))
+    rows = np.r_[0:8, M // 2:M // 2 + 8, M - 8:M]
+    assert oracle.rel_l2(y[rows], _ref64(x[rows], qw, qz, sc, None, g, x_dt, x_dt)) <= TOL_MFMA
+
+
 # Llama-3-70B projections (8192 -> 8192, 8192 -> 1024, 8192 -> 28672,
 # 28672 -> 8192), g128, fp16 activations N(0,1) and f16 scales, f16 output,
 # from decode (M = 1, 8) to prefill (M = 128 .. 4096). Outputs are checked on
