@@ -1,5 +1,7 @@
 // awq_gemv.hip -- decode path (M <= 8, and 9..16 rows on the matrix cores) of
-// the fused AWQ dequant-GEMM for gfx950.
+// the fused AWQ dequant-GEMM for gfx950: gemv_kernel (VALU, 1 row and small
+// 2-row problems), gemv_m4_kernel (2..4 rows, 4x4x4 matrix-core blocks),
+// gemv_mfma_kernel (5..16 rows, 16x16x32 matrix-core tile).
 //
 // y[m, n] = sum_k x[m, k] * (q[k, n] - z[k/g, n]) * s[k/g, n]   (AutoAWQ nibble order)
 // The reference's gemm_awq_decode (src/kernel/awq_kernel_gemm.rs:445-624) runs
@@ -430,6 +432,109 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t i, float (&v)[8])
   }
 }
 
+// Sum a workgroup's slot-order partials over its LDS slots (fixed order),
+// publish them across K splits (agent-scope stores, completion wait, arrival
+// count; the last workgroup of the chunk sums the splits in order), add the
+// bias and store rows < rows of the chunk's 512 columns. red[w][m][8 p + c]
+// holds packed lane c of pack p (column c in sequential order,
+// kAwqColOfLane[c] in AutoAWQ order).
+template <int MV, int WAVES, int kSlots, bool ACT>
+__device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*red)[MV][512], int* s_last_p,
+                                             int rows, bool seq) {
+  constexpr int kChunkCols = 512;
+  const int chunk = blockIdx.x;
+  const int split = blockIdx.y;
+  int& s_last = *s_last_p;
+  constexpr int kOut = MV * kChunkCols;
+  constexpr int kPer = (kOut + 64 * WAVES - 1) / (64 * WAVES);
+  float res[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = threadIdx.x + i * 64 * WAVES;
+    float v = 0.f;
+    if (o < kOut) {
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      // column c of its pack sits in slot c (sequential) or kAwqLaneOfCol[c]
+      // = (c >> 1) + 4 (c & 1) (AutoAWQ)
+      const int cs = (c & ~7) | (seq ? (c & 7) : ((c & 7) >> 1) + 4 * (c & 1));
+#pragma unroll
+      for (int ww = 0; ww < kSlots; ++ww) v += red[ww][m][cs];
+    }
+    res[i] = v;
+  }
+
+  const int col_base = chunk * kChunkCols;
+  if (a.splits > 1) {
+    // Same handshake as the VALU path: agent-scope partial stores, completion
+    // wait, arrival count; the last workgroup sums the splits in order.
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int o = threadIdx.x + i * 64 * WAVES;
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      if (o < kOut && m < rows && col_base + c < a.N)
+        __hip_atomic_store(&a.partial[((int64_t)split * MV + m) * a.N + col_base + c], res[i],
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCounterStride], 1u,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    // Each thread's kPer outputs, kSB splits at a time: kPer * kSB loads in
+    // flight (one output after another would leave one CU latency-bound on
+    // splits x rows x 2 KB); every output still sums its splits in order.
+    constexpr int kSB = kPer >= 16 ? 4 : 8;
+    const int64_t stride = (int64_t)MV * a.N;
+    const float* src[kPer];
+    bool ok[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int o = threadIdx.x + i * 64 * WAVES;
+      const int m = o / kChunkCols, c = o % kChunkCols;
+      ok[i] = o < kOut && m < rows && col_base + c < a.N;
+      // Rows past M read row M-1's partials (cached, discarded): unconditional
+      // loads keep the batch in flight.
+      src[i] = a.partial + (int64_t)min(m, rows - 1) * a.N + min(col_base + c, a.N - 1);
+      res[i] = 0.f;
+    }
+    for (int s0 = 0; s0 < a.splits; s0 += kSB) {
+      float t[kPer][kSB];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+#pragma unroll
+        for (int j = 0; j < kSB; ++j) {
+          const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
+          t[i][j] = __hip_atomic_load(src[i] + sj * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+#pragma unroll
+        for (int j = 0; j < kSB; ++j)
+          if (s0 + j < a.splits) res[i] += t[i][j];
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
+  // and its xor-1 neighbour.
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int o = threadIdx.x + i * 64 * WAVES;
+    const int m = o / kChunkCols, c = o % kChunkCols;
+    const int n = col_base + c;
+    float v = res[i];
+    if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
+    const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
+    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
+  }
+}
+
 template <int XT, int MV, int WAVES, int RPW, bool ACT>
 __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   constexpr int kChunkCols = 512;
@@ -603,94 +708,156 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   pack_set(std::integral_constant<int, 3>{});
   __syncthreads();
 
-  constexpr int kOut = MV * kChunkCols;
-  constexpr int kPer = (kOut + 64 * WAVES - 1) / (64 * WAVES);
-  float res[kPer];
+  finish_chunk<MV, WAVES, kSlots, ACT>(a, red, &s_last, rows, seq);
+}
+
+// ---------------------------------------------------------------------------
+// 2..8 rows on 4x4x4 matrix-core blocks (v_mfma_f32_4x4x4_16b_f16), in the
+// VALU path's own layout: lane l owns packed word chunk*64 + l of each of
+// the wave's RPW rows, one 256-byte row segment per load, and keeps it. The
+// 16 blocks of one instruction are lanes 4b .. 4b + 3: lane 4b + i supplies
+// row i of A (4 consecutive k of activation row i, the same for every
+// block) and column i of B (4 consecutive k of its own packed lane c, exact
+// f16 integers q - z: v_perm_b32 + v_bitop3_b32 + exact v_pk_add_f16 for
+// each pair of rows), and receives rows 0..3 of that column. So every lane
+// accumulates its own 8 columns for 4 activation rows with no transpose and
+// no padding: per 4 rows of W, 8 MFMAs per 4-row set of activations (twice
+// that with the low half of non-f16 activations), 1.5 VALU ops per weight.
+// Activations that are not f16 are scaled per row and wave by a power of two
+// and split as hi + lo in f16 exactly as in the 16x16x32 path above; the
+// scale is applied once per wave (its rows lie in one group).
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x4_t __attribute__((ext_vector_type(4)));
+
+template <int XT, int MV, int WAVES, int RPW, bool ACT>
+__global__ __launch_bounds__(64 * WAVES) void gemv_m4_kernel(GemvArgs a) {
+  constexpr int kChunkCols = 512;
+  constexpr bool kLo = XT != AWQ_F16;
+  constexpr int kSets = MV / 4;  // 4-row activation sets
+  constexpr int kQ = RPW / 4;    // 4-row steps of W per wave
+  static_assert(MV == 4 || MV == 8, "rows kept");
+  static_assert(RPW == 16 || RPW == 32 || RPW == 64, "rows per wave");
+  __shared__ float red[WAVES][MV][kChunkCols];
+  __shared__ int s_last;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int chunk = blockIdx.x;
+  const int split = blockIdx.y;
+  const int np = a.N >> 3;
+  const int rows = a.rows;
+  const int pack_c = min(chunk * 64 + lane, np - 1);  // clamped: loads stay in bounds
+
+  const int k0 = (split * WAVES + wave) * RPW;  // one run inside one group
+  const bool live = k0 < a.K;
+  const int kc = live ? k0 : 0;
+  const int grp = kc / a.group;
+
+  // ---- loads: the wave's RPW weight words, the zero word and scales of the
+  // lane's pack, then activation row (lane & 3) + 4 t over the same k.
+  const rsrc_t wr = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
+  const uint32_t voff = (uint32_t)pack_c * 4u;
+  const uint32_t row_bytes = (uint32_t)np * 4u;
+  uint32_t w[RPW];
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int o = threadIdx.x + i * 64 * WAVES;
-    float v = 0.f;
-    if (o < kOut) {
-      const int m = o / kChunkCols, c = o % kChunkCols;
-      // column c of its pack sits in slot c (sequential) or kAwqLaneOfCol[c]
-      // = (c >> 1) + 4 (c & 1) (AutoAWQ)
-      const int cs = (c & ~7) | (seq ? (c & 7) : ((c & 7) >> 1) + 4 * (c & 1));
+  for (int r = 0; r < RPW; ++r) w[r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + r) * row_bytes);
+  const uint32_t zw = a.qzeros[(int64_t)grp * np + pack_c];
+  const RawScales sraw = load_scales_raw(a.scales, a.st, (int64_t)grp * a.N + (int64_t)pack_c * 8);
+  const int ai = lane & 3;
+  float xv[kSets][RPW];
 #pragma unroll
-      for (int ww = 0; ww < kSlots; ++ww) v += red[ww][m][cs];
+  for (int t = 0; t < kSets; ++t) {
+    const int m = ai + 4 * t;
+    const int64_t base = (int64_t)min(m, rows - 1) * a.K + kc;
+#pragma unroll
+    for (int j = 0; j < RPW; j += 8) {
+      float v8[8];
+      load_x8<XT>(a.x, base + j, v8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[t][j + e] = m < rows ? v8[e] : 0.f;
     }
-    res[i] = v;
+  }
+  // Row scale (non-f16 activations): this row's largest |x| over the wave's
+  // rows to [2^14, 2^15); D row r of every block is A row r, held by lane r.
+  float xdown[kSets][4];
+#pragma unroll
+  for (int t = 0; t < kSets; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) xdown[t][r] = 1.f;
+  if constexpr (kLo) {
+#pragma unroll
+    for (int t = 0; t < kSets; ++t) {
+      float mx = 0.f;
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) mx = fmaxf(mx, fabsf(xv[t][j]));
+      int ex;
+      (void)frexpf(mx, &ex);  // mx = f * 2^ex, f in [0.5, 1)
+      const int up = min(max(15 - ex, -126), 127);
+      const float fup = ldexpf(1.f, up);
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) xv[t][j] *= fup;
+      const float down = ldexpf(1.f, -up);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) xdown[t][r] = __shfl(down, r, 64);
+    }
+  }
+  f16x4_t ahi[kSets][kQ], alo[kSets][kQ];
+#pragma unroll
+  for (int t = 0; t < kSets; ++t)
+#pragma unroll
+    for (int q = 0; q < kQ; ++q)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = xv[t][4 * q + e];
+        const _Float16 h = (_Float16)v;
+        ahi[t][q][e] = h;
+        if constexpr (kLo) alo[t][q][e] = (_Float16)(v - (float)h);
+      }
+
+  // ---- MFMAs: acc[t][c][r] = sum_k x[r + 4 t, k] * (q - z)[k, packed lane c]
+  f32x4_t acc[kSets][8];
+#pragma unroll
+  for (int t = 0; t < kSets; ++t)
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[t][c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f16x2 fz[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) fz[c] = __builtin_bit_cast(f16x2, nib_f16x2(zw, zw, c));
+#pragma unroll
+  for (int q = 0; q < kQ; ++q) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const f16x2 d01 = __builtin_bit_cast(f16x2, nib_f16x2(w[4 * q], w[4 * q + 1], c)) - fz[c];
+      const f16x2 d23 = __builtin_bit_cast(f16x2, nib_f16x2(w[4 * q + 2], w[4 * q + 3], c)) - fz[c];
+      const f16x4_t bq = f16x4_t{d01[0], d01[1], d23[0], d23[1]};
+#pragma unroll
+      for (int t = 0; t < kSets; ++t) {
+        acc[t][c] = __builtin_amdgcn_mfma_f32_4x4x4f16(ahi[t][q], bq, acc[t][c], 0, 0, 0);
+        if constexpr (kLo) acc[t][c] = __builtin_amdgcn_mfma_f32_4x4x4f16(alo[t][q], bq, acc[t][c], 0, 0, 0);
+      }
+    }
   }
 
-  const int col_base = chunk * kChunkCols;
-  if (a.splits > 1) {
-    // Same handshake as the VALU path: agent-scope partial stores, completion
-    // wait, arrival count; the last workgroup sums the splits in order.
+  // ---- scale (slot c takes the scale of its column), this wave's LDS slot ----
+  const bool seq = a.seq != 0;
+  float sl[8], slp[8];
+  scales_to_f32(sraw, a.st, sl);
 #pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int o = threadIdx.x + i * 64 * WAVES;
-      const int m = o / kChunkCols, c = o % kChunkCols;
-      if (o < kOut && m < rows && col_base + c < a.N)
-        __hip_atomic_store(&a.partial[((int64_t)split * MV + m) * a.N + col_base + c], res[i],
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int c = 0; c < 8; ++c) slp[c] = seq ? sl[c] : sl[awq_col_of_lane(c)];
+#pragma unroll
+  for (int t = 0; t < kSets; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float o[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) o[c] = live ? acc[t][c][r] * slp[c] * xdown[t][r] : 0.f;
+      float4* d4 = reinterpret_cast<float4*>(&red[wave][4 * t + r][8 * lane]);
+      d4[0] = make_float4(o[0], o[1], o[2], o[3]);
+      d4[1] = make_float4(o[4], o[5], o[6], o[7]);
     }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (threadIdx.x == 0) {
-      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCounterStride], 1u,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    // Each thread's kPer outputs, kSB splits at a time: kPer * kSB loads in
-    // flight (one output after another would leave one CU latency-bound on
-    // splits x rows x 2 KB); every output still sums its splits in order.
-    constexpr int kSB = kPer >= 16 ? 4 : 8;
-    const int64_t stride = (int64_t)MV * a.N;
-    const float* src[kPer];
-    bool ok[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int o = threadIdx.x + i * 64 * WAVES;
-      const int m = o / kChunkCols, c = o % kChunkCols;
-      ok[i] = o < kOut && m < rows && col_base + c < a.N;
-      // Rows past M read row M-1's partials (cached, discarded): unconditional
-      // loads keep the batch in flight.
-      src[i] = a.partial + (int64_t)min(m, rows - 1) * a.N + min(col_base + c, a.N - 1);
-      res[i] = 0.f;
-    }
-    for (int s0 = 0; s0 < a.splits; s0 += kSB) {
-      float t[kPer][kSB];
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-#pragma unroll
-        for (int j = 0; j < kSB; ++j) {
-          const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
-          t[i][j] = __hip_atomic_load(src[i] + sj * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-#pragma unroll
-        for (int j = 0; j < kSB; ++j)
-          if (s0 + j < a.splits) res[i] += t[i][j];
-    }
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-  }
+  __syncthreads();
 
-  // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
-  // and its xor-1 neighbour.
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int o = threadIdx.x + i * 64 * WAVES;
-    const int m = o / kChunkCols, c = o % kChunkCols;
-    const int n = col_base + c;
-    float v = res[i];
-    if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
-    const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
-    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
-  }
+  finish_chunk<MV, WAVES, WAVES, ACT>(a, red, &s_last, rows, seq);
 }
 
 int env_int(const char* name, int dflt) {
@@ -857,6 +1024,65 @@ void launch_mfma(const GemmProblem& p) {
   return launch_mfma_cfg<XT, MV, 4, 32>(p);
 }
 
+template <int XT, int MV, int WAVES, int RPW>
+void launch_m4_cfg(const GemmProblem& p) {
+  const int np = (int)(p.N / 8);
+  const int chunks = (np + 63) / 64;
+  const int splits = (int)((p.K + WAVES * RPW - 1) / (WAVES * RPW));
+  GemvArgs a{};
+  a.x = p.x;
+  a.qweight = p.qweight;
+  a.qzeros = p.qzeros;
+  a.scales = p.scales;
+  a.bias = p.bias;
+  a.y = p.y;
+  a.st = p.st;
+  a.bt = p.bt;
+  a.yt = p.yt;
+  a.rows = (int32_t)p.rows;
+  a.K = (int32_t)p.K;
+  a.N = (int32_t)p.N;
+  a.group = (int32_t)p.group;
+  a.splits = splits;
+  a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  if (splits > 1) {
+    const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
+    const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
+    a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
+    a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
+  }
+  if (p.act)
+    hipLaunchKernelGGL((gemv_m4_kernel<XT, MV, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES), 0,
+                       p.stream, a);
+  else
+    hipLaunchKernelGGL((gemv_m4_kernel<XT, MV, WAVES, RPW, false>), dim3(chunks, splits), dim3(64 * WAVES), 0,
+                       p.stream, a);
+  check_hip(hipGetLastError(), "gemv m4 kernel launch");
+}
+
+// 4x4x4 matrix-core decode: 16 waves x 32 rows for 4 rows of f16
+// activations (the only case whose registers, <= 128 VGPRs, and LDS slots,
+// 16 x 4 rows x 2 KB, allow 16 waves); otherwise 8 waves of 64 rows when
+// that gives 192..511 workgroups (and the group allows 64), else 8 x 32.
+// Measured with f32 activations at 2..4 rows: 64 rows at 4096 -> 14336 and
+// 14336 -> 4096 (224 workgroups) 5-12 % faster than 32; 32 rows where 64
+// gives 64 or >= 896 workgroups (4096 -> 4096, 28672 -> 8192) 10-15 % faster.
+template <int XT, int MV>
+void launch_m4(const GemmProblem& p) {
+  constexpr bool k16 = MV == 4 && XT == AWQ_F16;
+  const int64_t chunks = (p.N / 8 + 63) / 64;
+  const int64_t wgs64 = chunks * ((p.K + 511) / 512);
+  int waves = k16 ? 16 : 8;
+  int rpw = (!k16 && p.group % 64 == 0 && wgs64 >= 192 && wgs64 < 512) ? 64 : 32;
+  if (int v = env_int("AWQ_M4_WAVES", 0); v == 8 || (v == 16 && k16)) waves = v;
+  if (int v = env_int("AWQ_M4_RPW", 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
+  if constexpr (k16) {
+    if (waves == 16) return launch_m4_cfg<XT, MV, 16, 32>(p);
+  }
+  if (rpw == 64) return launch_m4_cfg<XT, MV, 8, 64>(p);
+  return launch_m4_cfg<XT, MV, 8, 32>(p);
+}
+
 template <int XT>
 void launch_xt(const GemmProblem& p) {
   // 2..8 rows: matrix cores, whose cost per weight does not grow with M,
@@ -869,6 +1095,12 @@ void launch_xt(const GemmProblem& p) {
   const bool mfma_ok = p.rows >= 2 && p.group % 32 == 0 && p.K % 32 == 0 &&
                        (force == 1 || (force != 0 && !small2));
   if (p.rows > 8) return launch_mfma<XT, 16>(p);  // accepted by small_m_mfma_ok
+  // 2..4 rows: the 4x4x4 blocks (no padding to 16 rows, no transposes):
+  // 4096 -> 14336 at M = 4 15.2 -> 11.4 us with f16 activations, 16.3 ->
+  // 14.6 with f32; 5..8 rows stay on the 16x16x32 kernel (at 8 rows the
+  // 4x4x4 MFMAs, twice as many, measured 5-45 % slower). AWQ_DECODE_M4=0
+  // forces the 16x16x32 kernel.
+  if (mfma_ok && p.rows <= 4 && env_int("AWQ_DECODE_M4", 1) != 0) return launch_m4<XT, 4>(p);
   if (mfma_ok) {
     // Rows kept in LDS, the workspace and the final reduction (the MFMA
     // tile always computes 16).

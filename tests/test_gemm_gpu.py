@@ -354,13 +354,21 @@ def test_prefill_tile_raster_groups(dev, monkeypatch, group_m):
     assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, "f16", "f16")) <= TOL_MFMA
 
 
-# Decode rows 2..8 run on the matrix cores by default; AWQ_DECODE_MFMA=0
-# selects the VALU kernel. Both are checked, in every launch configuration.
-@pytest.mark.parametrize("mfma", ["1", "0"])
+# Decode rows 2..8 run on the matrix cores by default (2..4 rows on 4x4x4
+# blocks, 5..8 on the 16-row tile); AWQ_DECODE_M4=0 sends 2..4 rows to the
+# 16-row tile and AWQ_DECODE_MFMA=0 selects the VALU kernel. All three are
+# checked, and every launch configuration below.
+DECODE_KERNELS = {"m4": {"AWQ_DECODE_MFMA": "1", "AWQ_DECODE_M4": "1"},
+                  "mfma16": {"AWQ_DECODE_MFMA": "1", "AWQ_DECODE_M4": "0"},
+                  "valu": {"AWQ_DECODE_MFMA": "0"}}
+
+
+@pytest.mark.parametrize("kernel", ["m4", "mfma16", "valu"])
 @pytest.mark.parametrize("M", [2, 3, 4, 7, 8])
 @pytest.mark.parametrize("x_dt", ["f32", "f16", "bf16"])
-def test_decode_rows_both_kernels(dev, monkeypatch, mfma, M, x_dt):
-    monkeypatch.setenv("AWQ_DECODE_MFMA", mfma)
+def test_decode_rows_both_kernels(dev, monkeypatch, kernel, M, x_dt):
+    for k, v in DECODE_KERNELS[kernel].items():
+        monkeypatch.setenv(k, v)
     K, N, g = 2048, 2080, 128  # N not a multiple of 512: partial column chunk
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
     y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32")
@@ -371,6 +379,7 @@ def test_decode_rows_both_kernels(dev, monkeypatch, mfma, M, x_dt):
 @pytest.mark.parametrize("waves,rpw", [(8, 64), (8, 32), (4, 64), (4, 32)])
 @pytest.mark.parametrize("s_dt", ["f32", "f16", "bf16"])
 def test_decode_mfma_every_configuration(dev, monkeypatch, waves, rpw, s_dt):
+    # 5 rows: the 16-row matrix-core tile (2..4 rows take the 4x4x4 blocks)
     monkeypatch.setenv("AWQ_MFMA_WAVES", str(waves))
     monkeypatch.setenv("AWQ_MFMA_RPW", str(rpw))
     M, K, N, g = 5, 4096, 1536, 64
@@ -380,10 +389,30 @@ def test_decode_mfma_every_configuration(dev, monkeypatch, waves, rpw, s_dt):
     assert oracle.rel_l2(to_host(y), ref) <= TOL_FP32
 
 
+@pytest.mark.parametrize("waves,rpw", [(16, 32), (8, 64), (8, 32)])
+@pytest.mark.parametrize("x_dt,s_dt", [("f32", "f16"), ("f16", "f16"), ("bf16", "bf16"), ("f32", "f32")])
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_decode_m4_every_configuration(dev, monkeypatch, waves, rpw, x_dt, s_dt, M):
+    """The 4x4x4 decode kernel in each launch configuration (16 waves only
+    with f16 activations; others fall back to 8), with bias, K splits and a
+    partial column chunk."""
+    monkeypatch.setenv("AWQ_DECODE_MFMA", "1")
+    monkeypatch.setenv("AWQ_M4_WAVES", str(waves))
+    monkeypatch.setenv("AWQ_M4_RPW", str(rpw))
+    K, N, g = 4096, 1536, 64
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, "f32")
+    ref = _ref64(x, qw, qz, sc, b, g, x_dt, s_dt)
+    assert oracle.rel_l2(to_host(y), ref) <= TOL_FP32
+
+
 @pytest.mark.parametrize("row_scales", [(1e6, 1e-6, 1.0, 3e4), (1e30, 1e-30, 7e4, 1e-20), (65504.0, 1e5, 2e-8, 1.0)])
-def test_decode_mfma_activation_magnitudes(dev, row_scales):
+@pytest.mark.parametrize("kernel", ["m4", "mfma16"])
+def test_decode_mfma_activation_magnitudes(dev, monkeypatch, row_scales, kernel):
     """fp32 activations far outside the f16 range, and far below it, in
     different rows of one call: each output row keeps fp32 accuracy."""
+    for k, v in DECODE_KERNELS[kernel].items():
+        monkeypatch.setenv(k, v)
     M, K, N, g = 4, 1024, 1024, 128
     x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f32", s_dt="f16")
     x = (x * np.asarray(row_scales, dtype=np.float64)[:, None]).astype(np.float32)

@@ -46,7 +46,7 @@ def _run(dev, x, qw, qz, sc, b, M, K, N, g, dt, order, y_dt=None):
     return to_host(y)
 
 
-@pytest.mark.parametrize("M", [1, 2, 5, 8, 9, 64, 300])
+@pytest.mark.parametrize("M", [1, 2, 3, 5, 8, 9, 64, 300])
 @pytest.mark.parametrize("dt", ["f32", "f16", "bf16"])
 def test_sequential_matches_oracle_and_autoawq_bits(dev, M, dt):
     K, N, g = 1024, 1056, 64

@@ -52,7 +52,8 @@ ROUTES = [
     (1, "f32", {}),                                   # decode GEMV (VALU)
     (3, "f32", {}),
     (8, "f32", {}),
-    (4, "f16", {}),                                   # decode on matrix cores
+    (4, "f16", {}),                                   # decode on 4x4x4 matrix-core blocks
+    (3, "bf16", {"AWQ_DECODE_M4": "0"}),              # decode on the 16-row matrix-core tile
     (8, "bf16", {}),
     (12, "f32", {}),                                  # 9..16 rows, matrix cores
     (16, "f16", {}),
