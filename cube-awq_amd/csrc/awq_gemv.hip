@@ -1116,9 +1116,12 @@ void launch_xt(const GemmProblem& p) {
 
 }  // namespace
 
+// 9..16 rows (prefill by the reference's M > 8 rule) on the decode kernels'
+// 16-row tile, unless the skinny kernel takes them (f16/bf16 activations on
+// outputs it suits). AWQ_SMALLM_MFMA=0 sends them to the prefill kernels.
 bool small_m_mfma_ok(const GemmProblem& p, int64_t launch_m) {
   return launch_m > 8 && launch_m <= 16 && p.rows <= 16 && p.group % 32 == 0 && p.K % 32 == 0 &&
-         env_int("AWQ_SMALLM_MFMA", 1) != 0;
+         env_int("AWQ_SMALLM_MFMA", 1) != 0 && !skinny_ok(p);
 }
 
 void launch_gemv(const GemmProblem& p) {

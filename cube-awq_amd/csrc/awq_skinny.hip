@@ -537,13 +537,15 @@ bool skinny_ok(const GemmProblem& p) {
   // (measured at K 4096..28672, N 1024..28672, 17..128 rows): wide outputs,
   // whose many column chunks fill the CUs with few K splits (1.1-2.7x at
   // N >= 6144), and on narrower ones up to 32 rows (1.1-1.5x), or 64 rows
-  // with K >= 8192. AWQ_SKINNY=0/1 forces the choice.
+  // with K >= 8192. 9..16 rows of f16/bf16 also come here instead of the
+  // decode kernels' 16-row tile (f16 0-28 % faster at K 4096..28672,
+  // N 1024..28672; bf16 -8..+20 %). AWQ_SKINNY=0/1 forces the choice.
   const int force = env_int("AWQ_SKINNY", -1);
   const bool wins = p.N >= 6144 || (p.N >= 1024 && (p.rows <= 32 || (p.rows <= 64 && p.K >= 8192)));
   if (force == 0 || (force != 1 && !wins)) return false;
   // bf16 activations need 16-bit scales (z s exact in f32, see the kernel).
   const bool types = p.xt == AWQ_F16 || (p.xt == AWQ_BF16 && p.st != AWQ_F32);
-  return types && p.rows > 16 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
+  return types && p.rows > 8 && p.rows <= 128 && p.K % kStep == 0 && p.group % kStep == 0 &&
          p.N % 32 == 0 && p.K * (p.N / 8) * 4 < (1ll << 32) && p.rows * p.K * 2 < (1ll << 32) &&
          (p.K / p.group) * p.N * 4 < (1ll << 32);
 }

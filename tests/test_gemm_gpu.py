@@ -423,18 +423,26 @@ def test_decode_mfma_activation_magnitudes(dev, monkeypatch, row_scales, kernel)
         assert oracle.rel_l2(y[m], ref[m]) <= TOL_FP32, (m, row_scales[m])
 
 
-# 9..16 rows run on the matrix-core decode kernel's 16-row tile (two-round
-# LDS reduction); AWQ_SMALLM_MFMA=0 sends them to the prefill kernels.
-@pytest.mark.parametrize("path", ["1", "0"])
+# 9..16 rows: f16/bf16 activations on the skinny kernel by default, fp32 on
+# the matrix-core decode kernel's 16-row tile (two-round LDS reduction, exact
+# q - z operands: fp32-level accuracy for every activation type);
+# AWQ_SKINNY=0 puts f16/bf16 on that tile too, and with AWQ_SMALLM_MFMA=0 as
+# well they go to the large-tile prefill kernels. All three are checked.
+SMALL_M_PATHS = {"default": {}, "tile16": {"AWQ_SKINNY": "0"},
+                 "tiles": {"AWQ_SMALLM_MFMA": "0", "AWQ_SKINNY": "0"}}
+
+
+@pytest.mark.parametrize("path", ["default", "tile16", "tiles"])
 @pytest.mark.parametrize("M", [9, 12, 16])
 @pytest.mark.parametrize("x_dt", ["f32", "f16", "bf16"])
 def test_small_m_both_paths(dev, monkeypatch, path, M, x_dt):
-    monkeypatch.setenv("AWQ_SMALLM_MFMA", path)
+    for k, v in SMALL_M_PATHS[path].items():
+        monkeypatch.setenv(k, v)
     K, N, g = 2048, 2080, 64
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
     y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32")
     ref = _ref64(x, qw, qz, sc, b, g, x_dt, "f16")
-    tol = TOL_FP32 if (path == "1" or x_dt == "f32") else TOL_MFMA
+    tol = TOL_FP32 if (path == "tile16" or x_dt == "f32") else TOL_MFMA
     assert oracle.rel_l2(to_host(y), ref) <= tol
 
 
@@ -447,10 +455,11 @@ def test_small_m_every_configuration(dev, monkeypatch, rpw):
     assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, None, g, "f32", "f32")) <= TOL_FP32
 
 
-# 17..128 rows of f16 or bf16 activations (16-bit scales) run on the skinny
-# kernel (awq_skinny.hip); AWQ_SKINNY=0 sends them to the large-tile kernels.
+# 9..128 rows of f16 or bf16 activations (16-bit scales) run on the skinny
+# kernel (awq_skinny.hip); AWQ_SKINNY=0 sends them to the large-tile kernels
+# (17..128 rows) or the 16-row decode tile (9..16).
 @pytest.mark.parametrize("path", ["1", "0"])
-@pytest.mark.parametrize("M", [17, 33, 48, 64, 80, 96, 100, 128])
+@pytest.mark.parametrize("M", [9, 16, 17, 33, 48, 64, 80, 96, 100, 128])
 @pytest.mark.parametrize("x_dt", ["f16", "bf16"])
 def test_skinny_both_paths(dev, monkeypatch, path, M, x_dt):
     monkeypatch.setenv("AWQ_SKINNY", path)
@@ -474,7 +483,7 @@ def test_skinny_every_split(dev, monkeypatch, splits, x_dt, s_dt, g):
     assert oracle.rel_l2(host_f32(y, y_dt), _ref64(x, qw, qz, sc, b, g, x_dt, s_dt)) <= TOL_MFMA
 
 
-@pytest.mark.parametrize("M", [48, 128])
+@pytest.mark.parametrize("M", [12, 48, 128])
 @pytest.mark.parametrize("splits", ["1", "3"])
 @pytest.mark.parametrize("x_dt,s_dt", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f16"), ("f16", "bf16")])
 def test_skinny_weights_exact(dev, monkeypatch, M, splits, x_dt, s_dt):

@@ -56,7 +56,8 @@ ROUTES = [
     (3, "bf16", {"AWQ_DECODE_M4": "0"}),              # decode on the 16-row matrix-core tile
     (8, "bf16", {}),
     (12, "f32", {}),                                  # 9..16 rows, matrix cores
-    (16, "f16", {}),
+    (16, "f16", {}),                                  # 9..16 rows of f16: skinny
+    (16, "f16", {"AWQ_SKINNY": "0"}),                 # 9..16 rows on the 16-row tile
     (17, "f16", {}),                                  # skinny, split-K
     (64, "f16", {"AWQ_SKINNY_SPLITS": "1"}),          # skinny, direct store
     (100, "f16", {}),
