@@ -1160,6 +1160,24 @@ void launch_gemm(const GemmProblem& p) {
              "prefill GEMM: tensor too large");
   const int64_t tiles = ((p.rows + 127) / 128) * ((p.N + 127) / 128);
   AWQ_ASSERT(tiles < (1ll << 31), "prefill GEMM: too many tiles");
+  // fp32 activations, 17..256 rows: 16-row slices, each one launch of the
+  // decode kernels' 16-row matrix-core tile (x split as hi + lo in f16 with a
+  // per-row power-of-two scale, exact q - z operands: fp32-level accuracy),
+  // in order on the stream. The 128 x 128 fp32-MFMA kernel has too few tiles
+  // there to fill the CUs: 4096 -> 14336 at M = 17..256 took 373..413 us,
+  // 14336 -> 4096 1287..1354 us, against about 20..28 us per slice.
+  if (p.xt == AWQ_F32 && p.rows > 16 && p.rows <= 256 && p.group % 32 == 0 && p.K % 32 == 0 &&
+      env_int("AWQ_F32_SLICES", 1) != 0) {
+    const int64_t y_row = (p.act ? p.N / 2 : p.N) * dtype_size(p.yt);
+    for (int64_t r0 = 0; r0 < p.rows; r0 += 16) {
+      GemmProblem q = p;
+      q.rows = std::min<int64_t>(16, p.rows - r0);
+      q.x = static_cast<const char*>(p.x) + r0 * p.K * 4;
+      q.y = static_cast<char*>(p.y) + r0 * y_row;
+      launch_gemv(q);
+    }
+    return;
+  }
   if (skinny_ok(p)) return launch_skinny(p);
   switch (p.xt) {
     case AWQ_F16: launch_st<MODE_F16>(p); break;

@@ -446,6 +446,23 @@ def test_small_m_both_paths(dev, monkeypatch, path, M, x_dt):
     assert oracle.rel_l2(to_host(y), ref) <= tol
 
 
+# fp32 activations at 17..256 rows run as 16-row slices on the decode
+# kernels' 16-row tile; AWQ_F32_SLICES=0 sends them to the fp32-MFMA prefill
+# kernel. Both, with a ragged last slice (1..15 rows, so also the smaller
+# decode kernels), bias and every output dtype.
+@pytest.mark.parametrize("path", ["1", "0"])
+@pytest.mark.parametrize("M,y_dt", [(17, "f32"), (33, "f16"), (100, "bf16"), (256, "f32")])
+def test_f32_rows_slices_and_prefill_kernel(dev, monkeypatch, path, M, y_dt):
+    monkeypatch.setenv("AWQ_F32_SLICES", path)
+    K, N, g = 1024, 1056, 64
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f32", s_dt="f16", bias=True)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f32", "f16", y_dt))
+    ref = _ref64(x, qw, qz, sc, b, g, "f32", "f16")
+    # f16 / bf16 outputs: one rounding of relative size 2^-11 / 2^-8.
+    tol = {"f32": TOL_FP32, "f16": 1e-3, "bf16": 4e-3}[y_dt]
+    assert oracle.rel_l2(host_f32(y, y_dt), ref) <= tol
+
+
 @pytest.mark.parametrize("rpw", [32, 64])
 def test_small_m_every_configuration(dev, monkeypatch, rpw):
     monkeypatch.setenv("AWQ_MFMA_RPW", str(rpw))
