@@ -406,6 +406,22 @@ def test_decode_m4_every_configuration(dev, monkeypatch, waves, rpw, x_dt, s_dt,
     assert oracle.rel_l2(to_host(y), ref) <= TOL_FP32
 
 
+@pytest.mark.parametrize("K,N,g", [(64, 32, 64), (192, 64, 64), (4160, 544, 64), (320, 4096, 64)])
+@pytest.mark.parametrize("x_dt", ["f32", "f16"])
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_decode_m4_edge_shapes(dev, monkeypatch, K, N, g, x_dt, M):
+    """4x4x4 decode edge cases: one pack chunk with most lanes clamped
+    (N = 32), waves whose rows start past K (K not a multiple of a
+    workgroup's rows), one K split or many (g = 64: the reference's module
+    rule, group >= 64)."""
+    monkeypatch.setenv("AWQ_DECODE_MFMA", "1")
+    monkeypatch.setenv("AWQ_DECODE_M4", "1")
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32"))
+    assert np.isfinite(y).all()
+    assert oracle.rel_l2(y, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_FP32
+
+
 @pytest.mark.parametrize("row_scales", [(1e6, 1e-6, 1.0, 3e4), (1e30, 1e-30, 7e4, 1e-20), (65504.0, 1e5, 2e-8, 1.0)])
 @pytest.mark.parametrize("kernel", ["m4", "mfma16"])
 def test_decode_mfma_activation_magnitudes(dev, monkeypatch, row_scales, kernel):
