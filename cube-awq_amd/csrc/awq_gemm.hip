@@ -1160,14 +1160,29 @@ void launch_gemm(const GemmProblem& p) {
              "prefill GEMM: tensor too large");
   const int64_t tiles = ((p.rows + 127) / 128) * ((p.N + 127) / 128);
   AWQ_ASSERT(tiles < (1ll << 31), "prefill GEMM: too many tiles");
-  // fp32 activations, 17..256 rows: 16-row slices, each one launch of the
+  // fp32 activations, 17 or more rows: 16-row slices, each one launch of the
   // decode kernels' 16-row matrix-core tile (x split as hi + lo in f16 with a
   // per-row power-of-two scale, exact q - z operands: fp32-level accuracy),
-  // in order on the stream. The 128 x 128 fp32-MFMA kernel has too few tiles
-  // there to fill the CUs: 4096 -> 14336 at M = 17..256 took 373..413 us,
-  // 14336 -> 4096 1287..1354 us, against about 20..28 us per slice.
-  if (p.xt == AWQ_F32 && p.rows > 16 && p.rows <= 256 && p.group % 32 == 0 && p.K % 32 == 0 &&
-      env_int("AWQ_F32_SLICES", 1) != 0) {
+  // in order on the stream, where that beats the 128 x 128 fp32-MFMA kernel.
+  // That kernel runs about 6.1 us per 64-row stage of K per wave of tiles
+  // over the CUs (no K split), so with few tiles it is slow however few rows
+  // there are: 4096 -> 14336 at M = 17 373 us, 14336 -> 4096 1287 us. A slice
+  // costs about 12 us + its weight bytes at 2.4 TB/s. Slices for <= 256 rows
+  // (faster at every measured shape) and up to 1024 when that estimate is
+  // lower (measured 10-35 % faster up to 1024 rows at 4096 -> 14336 and
+  // 8192 -> 28672, up to 768 at 14336 -> 4096; slower past 256 at
+  // 4096 -> 4096, where the fp32 kernel's time stays flat).
+  const int f32_slices = env_int("AWQ_F32_SLICES", 1);  // 0: never, 2: at any row count
+  auto slices_win = [&]() {
+    if (p.rows <= 256 || f32_slices == 2) return true;
+    if (p.rows > 1024) return false;
+    const int64_t cus = device_cus();
+    const double generic = (double)((tiles + cus - 1) / cus) * (double)(p.K / 64) * 6.1;
+    const double slice = 12.0 + (double)p.K * (double)p.N / 2.0 / 2.4e6;
+    return (double)((p.rows + 15) / 16) * slice < generic;
+  };
+  if (p.xt == AWQ_F32 && p.rows > 16 && p.group % 32 == 0 && p.K % 32 == 0 && f32_slices != 0 &&
+      slices_win()) {
     const int64_t y_row = (p.act ? p.N / 2 : p.N) * dtype_size(p.yt);
     for (int64_t r0 = 0; r0 < p.rows; r0 += 16) {
       GemmProblem q = p;

@@ -462,12 +462,13 @@ def test_small_m_both_paths(dev, monkeypatch, path, M, x_dt):
     assert oracle.rel_l2(to_host(y), ref) <= tol
 
 
-# fp32 activations at 17..256 rows run as 16-row slices on the decode
-# kernels' 16-row tile; AWQ_F32_SLICES=0 sends them to the fp32-MFMA prefill
-# kernel. Both, with a ragged last slice (1..15 rows, so also the smaller
-# decode kernels), bias and every output dtype.
-@pytest.mark.parametrize("path", ["1", "0"])
-@pytest.mark.parametrize("M,y_dt", [(17, "f32"), (33, "f16"), (100, "bf16"), (256, "f32")])
+# fp32 activations at 17..256 rows (and up to 1024 where the launcher's
+# estimate prefers it) run as 16-row slices on the decode kernels' 16-row
+# tile; AWQ_F32_SLICES=0 sends them to the fp32-MFMA prefill kernel, 2 forces
+# slices at any row count. All three, with a ragged last slice (1..15 rows,
+# so also the smaller decode kernels), bias and every output dtype.
+@pytest.mark.parametrize("path", ["1", "0", "2"])
+@pytest.mark.parametrize("M,y_dt", [(17, "f32"), (33, "f16"), (100, "bf16"), (256, "f32"), (300, "f32")])
 def test_f32_rows_slices_and_prefill_kernel(dev, monkeypatch, path, M, y_dt):
     monkeypatch.setenv("AWQ_F32_SLICES", path)
     K, N, g = 1024, 1056, 64
