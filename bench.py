@@ -20,8 +20,10 @@ Method: inputs resident in HBM before timing; the decode rotates over
 ceil(512 MB / bytes-per-call) independent weight copies so the 256 MB MALL
 cannot serve them. Calls are captured in a HIP graph (one graph = many
 back-to-back launches on the stream) and the graph is replayed; HIP events on
-that stream bracket the timed replays, after `--warmup` untimed calls and a
-device synchronise on both sides. `roofline.achieved` = algorithmic bytes
+that stream bracket the timed replays, after untimed calls (`--warmup` for
+the decode; 200, about 50 ms, for the M=2048 prefill and the dense GEMM beside
+it, since the clock ramps up over tens of milliseconds of matrix-core work
+after the memory-bound phases) and a device synchronise on both sides. `roofline.achieved` = algorithmic bytes
 (flops) per launch / average launch duration from those events.
 cpu_baseline: the oracle's C restatement of the reference's f32 loop on the
 host cores (OpenMP), on a bounded sample of the same decode workload.
@@ -52,7 +54,63 @@ def parse():
                          "device copy used to calibrate the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--sweep", action="store_true",
+                    help="instead of the headline line: one JSON line per point of the decode sweep "
+                         "(Llama-3-8B shapes, M = 1, 4, 8, f32 x), the prefill sweep (Llama-3-8B "
+                         "shapes, M = 64, 512, 2048, f16 x) and the Llama-3-70B projections "
+                         "(M = 1, 8, 128, 1024, 4096, f16 x)")
     return ap.parse_args()
+
+
+# Sweep points: (name, x dtype, shapes K -> N, row counts), g128, f16 scales,
+# output in the activation dtype (f32 for the decode sweep).
+SWEEPS = [
+    ("decode_llama3_8b", "f32", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)], (1, 4, 8)),
+    ("prefill_llama3_8b", "f16", [(4096, 4096), (4096, 14336), (14336, 4096)], (64, 512, 2048)),
+    ("llama3_70b", "f16", [(8192, 8192), (8192, 1024), (8192, 28672), (28672, 8192)], (1, 8, 128, 1024, 4096)),
+]
+
+
+def sweep(dev, np, torch, synth, _lib, call_gemm, graph_time):
+    """One JSON line per (sweep, shape, M): time per call from HIP events over
+    graph-replayed launches on rotated weight copies (as the headline), GB/s
+    of algorithmic bytes K*N/2 + (K/g)*(N/8)*4 + (K/g)*N*2 + M*K*xs + M*N*ys,
+    TFLOP/s of 2*M*N*K, and both as fractions of the HBM and fp16 MFMA peaks."""
+    G = 128
+    dt = {"f32": (_lib.AWQ_F32, torch.float32, np.float32, 4), "f16": (_lib.AWQ_F16, torch.float16, np.float16, 2)}
+    for name, xdt, shapes, rows in SWEEPS:
+        xt, tdt, ndt, xs = dt[xdt]
+        for K, N in shapes:
+            qw = torch.from_numpy(synth.packed_nibbles(synth.TID_QWEIGHT, K, N // 8).view(np.int32)).to(dev)
+            qz = torch.from_numpy(synth.packed_nibbles(synth.TID_QZEROS, K // G, N // 8).view(np.int32)).to(dev)
+            sc = torch.from_numpy(synth.uniform(synth.TID_SCALES, (K // G, N), 0.002, 0.02, np.float16)).to(dev)
+            w_bytes = K * N // 2 + (K // G) * (N // 8) * 4 + (K // G) * N * 2
+            copies = max(1, math.ceil(512e6 / w_bytes))
+            ws = [(qw.clone(), qz.clone(), sc.clone()) for _ in range(copies)]
+            for M in rows:
+                x = torch.from_numpy(synth.normal(synth.TID_X, (M, K), ndt)).to(dev)
+                y = torch.empty((M, N), dtype=tdt, device=dev)
+
+                def launch(i, x=x, y=y, M=M):
+                    w = ws[i % copies]
+                    call_gemm(x, xt, w[0], w[1], w[2], _lib.AWQ_F16, y, xt, M, K, N, G)
+
+                flops = 2.0 * M * N * K
+                # at least ~10 ms of calls per point (the matrix cores settle at a
+                # power-limited clock after the first few milliseconds)
+                steps = 2000 if flops < 2e10 else 200 if flops < 5e11 else 50
+                warm = 5 if flops < 5e11 else 100  # clock ramp on long matrix-core runs
+                ms, _, _ = graph_time(launch, min(100, steps), warm, steps)
+                nbytes = w_bytes + M * K * xs + M * N * xs
+                gbs = nbytes / (ms * 1e-3) / 1e9
+                tflops = flops / (ms * 1e-3) / 1e12
+                print(json.dumps(dict(sweep=name, M=M, K=K, N=N, x=xdt, us=round(ms * 1e3, 2),
+                                      gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                                      tflops=round(tflops, 1),
+                                      mfma_frac=round(tflops / FP16_MFMA_PEAK_TFLOPS, 4))), flush=True)
+                del x, y
+            del ws, qw, qz, sc
+            torch.cuda.empty_cache()
 
 
 def main():
@@ -122,6 +180,10 @@ def main():
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / steps
         return ms, steps, wall
+
+    if args.sweep:
+        sweep(dev, np, torch, synth, _lib, call_gemm, graph_time)
+        return
 
     out = {}
     traffic = {}
@@ -251,8 +313,11 @@ def main():
         def pre(i):
             call_gemm(xp, _lib.AWQ_F16, qw, qz, sc, _lib.AWQ_F16, yp, _lib.AWQ_F16, PM, K, N, G)
 
-        steps = 50 if args.only is None else max(10, args.steps // 100)
-        ms, calls, wall = graph_time(pre, 10, 5, steps)
+        # 200 untimed calls (~50 ms) first: after the memory-bound decode phase
+        # the clock takes tens of milliseconds of matrix-core work to ramp up
+        # (measured: the first 50 calls averaged 285 us, the following ones 240).
+        steps = 100 if args.only is None else max(10, args.steps // 100)
+        ms, calls, wall = graph_time(pre, 10, 200, steps)
         out["prefill"] = dict(ms=ms, calls=calls, wall_s=wall, tflops=pf_flops / (ms * 1e-3) / 1e12)
         if args.only is None:
             # The other prefill rows of the same shape.
@@ -278,7 +343,7 @@ def main():
                 torch.matmul(xp, wd.t(), out=yd)
 
             try:
-                dms, _, _ = graph_time(dense, 10, 5, 50)
+                dms, _, _ = graph_time(dense, 10, 200, 100)  # same warm-up and count as the fused call
                 out["prefill"]["dense_tflops"] = pf_flops / (dms * 1e-3) / 1e12
             except RuntimeError as e:  # informational only: never fail the bench on it
                 print(f"dense comparison skipped: {e}", file=sys.stderr)
