@@ -21,6 +21,11 @@
 //    groups interleave a few VALU ops after each MFMA) and written to LDS
 //    n-major with k contiguous. One s_barrier per stage; waits are explicit
 //    vmcnt/lgkmcnt counts, so loads of later stages stay in flight.
+//  * 256x224 runs ping-pong (PP) by default: the two halves of the waves
+//    (one half of the rows each) run one phase apart, one half multiplying
+//    while the other reads its operands from LDS, issues the next loads and
+//    dequantises; two barriers per stage. Each accumulator's MFMAs keep the
+//    single-phase order, so both schedules give the same bits.
 //  * f16 dequant: one v_perm_b32 gathers the byte holding the column's lane
 //    from two rows, one v_bitop3_b32 forms f16 1024 + q (low nibble) or
 //    64 + q (high nibble), then an exact v_pk_add_f16 of the zero and one
@@ -446,7 +451,7 @@ struct BigTile {
   static_assert(kWTM % MS == 0 && kWTN % MS == 0, "wave tile must be whole MFMA blocks");
 };
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool ACT>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool ACT, bool PP>
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   using S = typename Elem<ST>::type;
@@ -485,12 +490,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // l >> 3, slot l & 7 of an 8-row chunk; so lane l fetches the granule that
   // belongs in that slot, (l & 7) ^ swz(row). Wave w fills chunks w + i*NW.
   constexpr int NW = C::kThreads / 64;
+  // PP (ping-pong): the two halves of the waves own the two halves of the
+  // rows, and each half loads only its own rows of X: wave w of half h fills
+  // chunks (BM/16) h + (w mod NW/2) + i NW/2.
   constexpr int kXIns = BM / 8 / NW;
+  auto xchunk = [&](int i) {
+    if constexpr (PP) return (wave / (NW / 2)) * (BM / 16) + wave % (NW / 2) + i * (NW / 2);
+    else return wave + i * NW;
+  };
   const rsrc_t xres = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
   uint32_t xvoff[kXIns];
 #pragma unroll
   for (int i = 0; i < kXIns; ++i) {
-    const int row = 8 * (wave + i * NW) + (lane >> 3);
+    const int row = 8 * xchunk(i) + (lane >> 3);
     const int grow = min(m0 + row, a.M - 1);  // rows past M read row M-1; never stored
     const int gran = (lane & 7) ^ swz<MS>(row);
     xvoff[i] = (uint32_t)(grow * a.K + gran * 8) * 2u;
@@ -553,7 +565,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     const uint32_t koff = (uint32_t)((s_begin + s) * kBK) * 2u;
 #pragma unroll
     for (int i = 0; i < kXIns; ++i) {
-      lds_dma16(xres, smem_raw + buf * C::kABytes + (wave + i * NW) * 1024, xvoff[i], koff);
+      lds_dma16(xres, smem_raw + buf * C::kABytes + xchunk(i) * 1024, xvoff[i], koff);
     }
   };
 
@@ -715,6 +727,101 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // two they were issued last in this stage and everything must land.
   constexpr int kVmWait = (kNA == 3) ? kVmPerStage : 0;
 
+  if constexpr (PP) {
+    // ---- ping-pong schedule ------------------------------------------------
+    // Half 0 (waves 0..NW/2-1, rows 0..BM/2-1) and half 1 (the other rows)
+    // run one phase apart: while one half multiplies, the other reads its
+    // operands from LDS, issues the loads of stage s+2 and dequantises
+    // W(s+1). Every stage is two phases, each closed by a barrier; half 1
+    // takes one extra barrier before its loop and half 0 one after, so the
+    // counts match. A memory phase of stage s of one half and the compute
+    // phase of stage s-1 (half 1) or s (half 0) of the other run together.
+    //   X: each half loads and reads only its own rows, three buffers, two
+    //      stages ahead (buffer (s+2) % 3 last held X(s-1), read by this half
+    //      in its memory phase s-1).
+    //   W: both halves dequantise W(s+1) into buffer (s+1) % 2 in memory
+    //      phase s. Its previous contents W(s-1) were read by half 0 before
+    //      the barrier that half 1's memory phase s-1 ends with, and by half 1
+    //      before its memory phase s-1 ended; W(s+1) is complete at the end of
+    //      half 1's memory phase s, before either half reads it in memory
+    //      phase s+1. So a stage's W operands are all read in its memory
+    //      phase; X of its second k-slice is read in the compute phase.
+    static_assert(kNA == 3 && WGM % 2 == 0 && (BM / 16) % (NW / 2) == 0 && MS == 16 && C::kSlices == 2,
+                  "ping-pong layout");
+    const bool h1 = wave >= NW / 2;
+    WRegs& wq_ = wr[0];  // one register set: W(s+2) is loaded once W(s+1) is dequantised
+    load_w(0, wq_);
+    load_x(0, 0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+#pragma unroll
+    for (int c = 0; c < 8; ++c) deq_store_col(wq_, c, 0);
+    load_x(min(1, stages - 1), 1);
+    load_w(min(1, stages - 1), wq_);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmPerStage, 0));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (h1) __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    auto read_a = [&](int xb, int kq, int i) {
+      return *reinterpret_cast<const V8*>(smem_raw + (a16[i] ^ (uint32_t)(kq << 6)) + xb * C::kABytes);
+    };
+    auto read_b = [&](int wb, int kq, int j) {
+      return *reinterpret_cast<const V8*>(smem_raw + (b16[j] ^ (uint32_t)(kq << 6)) + wb * C::kBBytes);
+    };
+    auto mma = [&](const V8& x, const V8& w, AccT& d) {
+      if constexpr (MODE == MODE_F16) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, w, d, 0, 0, 0);
+      else d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, w, d, 0, 0, 0);
+    };
+    auto step_pp = [&](int s, int xb, int wb) {
+      V8 fa[C::kI], fb0[C::kJ], fb1[C::kJ];
+      // Memory phase: W operands of both k-slices and X of the first.
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < C::kJ; ++j) fb0[j] = read_b(wb, 0, j);
+#pragma unroll
+      for (int j = 0; j < C::kJ; ++j) fb1[j] = read_b(wb, 1, j);
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i) fa[i] = read_a(xb, 0, i);
+      load_x(min(s + 2, stages - 1), (xb + 2) % 3);
+      // X(s+1) and W(s+1), issued in the previous memory phase, have landed.
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kXIns, 15));
+#pragma unroll
+      for (int c = 0; c < 8; ++c) deq_store_col(wq_, c, wb ^ 1);
+      load_w(min(s + 2, stages - 1), wq_);
+      __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmPerStage, 0));
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      // Compute phase: X of the second k-slice (rows private to this half)
+      // is read row block by row block into the registers the first slice
+      // has finished with.
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i) {
+#pragma unroll
+        for (int j = 0; j < C::kJ; ++j) mma(fa[i], fb0[j], acc[i][j]);
+        fa[i] = read_a(xb, 1, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::kJ; ++j) mma(fa[i], fb1[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+    for (int s = 0; s < stages; s += 6) {
+#pragma unroll
+      for (int u = 0; u < 6; ++u) {
+        if (u == 0 || s + u < stages) step_pp(s + u, u % 3, u % 2);
+      }
+    }
+    if (!h1) __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  } else {
   // ---- prologue ------------------------------------------------------------
   load_w(0, wr[0]);
   load_x(0, 0);
@@ -785,6 +892,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     for (int u = 0; u < kU; ++u) {
       if (u == 0 || s + u < stages) step(s + u, u % kNA, u % 2, wr[(u + 1) % 2], wr[u % 2]);
     }
+  }
   }
 
   // ---- epilogue --------------------------------------------------------------
@@ -922,7 +1030,7 @@ int raster_group_m(int tiles_m, int bm, int bn) {
   return a;
 }
 
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool ACT>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool ACT, bool PP>
 void launch_big_act(const GemmProblem& p, int splits) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   GemmArgs a{};
@@ -958,23 +1066,23 @@ void launch_big_act(const GemmProblem& p, int splits) {
   }
   static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
   if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT>,
+    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT, PP>,
                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kSmem),
               "hipFuncSetAttribute(gemm_big)");
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT>), dim3(tiles, a.splits),
+  hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT, PP>), dim3(tiles, a.splits),
                      dim3(C::kThreads), C::kSmem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
 }
 
 // The SiLU epilogue exists for the AutoAWQ order only (awq_gemm_silu_mul).
-template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ>
+template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, bool PP = false>
 void launch_big(const GemmProblem& p, int splits) {
   if constexpr (!SEQ) {
-    if (p.act) return launch_big_act<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, true>(p, splits);
+    if (p.act) return launch_big_act<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, true, PP>(p, splits);
   }
-  launch_big_act<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, false>(p, splits);
+  launch_big_act<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, false, PP>(p, splits);
 }
 
 template <int MODE, int ST, int BM, int BN, int WGM, int WGN, bool SEQ, bool ACT>
@@ -1042,14 +1150,14 @@ void launch_mode(const GemmProblem& p) {
   int splits = 1;
   if (cfg == 0) {
     // Whole waves of workgroups over the CUs matter at these sizes: 256 x 224
-    // tiles (16x16 MFMA blocks) when they fill the last wave better than
-    // 256 x 256, e.g. 2048 x 14336 = 512 tiles (two full waves on 256 CUs)
-    // instead of 448 (1.75).
+    // tiles (16x16 MFMA blocks, ping-pong schedule) when they fill the last
+    // wave better than 256 x 256, e.g. 2048 x 14336 = 512 tiles (two full
+    // waves on 256 CUs) instead of 448 (1.75).
     auto fill = [&](int64_t t) {
       const int64_t cus = device_cus();
       return (double)t / (double)(((t + cus - 1) / cus) * cus);
     };
-    if (tiles(256, 224) >= 240 && fill(tiles(256, 224)) > fill(tiles(256, 256)) + 0.05) cfg = 9;
+    if (tiles(256, 224) >= 240 && fill(tiles(256, 224)) > fill(tiles(256, 256)) + 0.05) cfg = 10;
     else if (tiles(256, 256) >= 240) cfg = 2;
     else if (tiles(128, 256) >= 200) cfg = 3;
     else {
@@ -1107,7 +1215,7 @@ void launch_mode(const GemmProblem& p) {
         return (double)(waves * st) * per_stage + partials;
       };
       struct Cand { int cfg, sp; double t; };
-      const Cand big[4] = {{9, 1, est(256, 224, 1, 1.9)}, {9, 2, est(256, 224, 2, 1.9)},
+      const Cand big[4] = {{10, 1, est(256, 224, 1, 1.9)}, {10, 2, est(256, 224, 2, 1.9)},
                            {2, 1, est(256, 256, 1, 2.1)}, {2, 2, est(256, 256, 2, 2.1)}};
       Cand b = big[0];
       for (const Cand& c : big)
@@ -1128,7 +1236,8 @@ void launch_mode(const GemmProblem& p) {
       case 6: return launch_big<MODE, ST, 256, 128, 4, 2, 32, SEQ>(p, splits);
       case 7: return launch_big<MODE, ST, 256, 256, 2, 2, 32, SEQ>(p, splits);
       case 8: return launch_big<MODE, ST, 64, 256, 1, 8, 32, SEQ>(p, splits);
-      case 9: return launch_big<MODE, ST, 256, 224, 4, 2, 16, SEQ>(p, splits);
+      case 9: return launch_big<MODE, ST, 256, 224, 4, 2, 16, SEQ>(p, splits);  // single-phase
+      case 10: return launch_big<MODE, ST, 256, 224, 4, 2, 16, SEQ, true>(p, splits);  // ping-pong
       default: break;
     }
   }

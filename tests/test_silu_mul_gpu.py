@@ -67,6 +67,7 @@ ROUTES = [
     (300, "f16", {}),                                 # large tiles, direct store
     (300, "bf16", {}),
     (300, "f16", {"AWQ_GEMM_TILE": "1"}),             # generic tiles
+    (300, "f16", {"AWQ_GEMM_TILE": "10"}),            # 256 x 224 tiles, ping-pong halves
     (40, "f32", {}),                                  # fp32 prefill
 ]
 
