@@ -796,7 +796,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       __builtin_amdgcn_sched_barrier(0);
       // Compute phase: X of the second k-slice (rows private to this half)
       // is read row block by row block into the registers the first slice
-      // has finished with.
+      // has finished with. Raised wave priority: the multiplying half wins
+      // issue over the half in its memory phase.
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < C::kI; ++i) {
 #pragma unroll
@@ -809,6 +811,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 #pragma unroll
         for (int j = 0; j < C::kJ; ++j) mma(fa[i], fb1[j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
