@@ -1152,15 +1152,17 @@ void launch_mode(const GemmProblem& p) {
   auto tiles = [&](int bm, int bn) { return ((p.rows + bm - 1) / bm) * ((p.N + bn - 1) / bn); };
   int splits = 1;
   if (cfg == 0) {
-    // Whole waves of workgroups over the CUs matter at these sizes: 256 x 224
-    // tiles (16x16 MFMA blocks, ping-pong schedule) when they fill the last
-    // wave better than 256 x 256, e.g. 2048 x 14336 = 512 tiles (two full
-    // waves on 256 CUs) instead of 448 (1.75).
-    auto fill = [&](int64_t t) {
+    // Whole waves of workgroups over the CUs matter at these sizes. A wave
+    // of 256 x 224 tiles (16x16 MFMA blocks, ping-pong schedule) costs about
+    // 0.85 of a wave of 256 x 256 tiles (measured 211 against 250 us per
+    // wave at 4096 x 8192 -> 28672), so they are taken when 0.85 x their
+    // waves is below the 256 x 256 waves: e.g. 2048 x 14336 = 2 waves of
+    // either, 4096 x 28672 8 against 7; not 4096 x 8192 (3 against 2).
+    auto waves = [&](int64_t t) {
       const int64_t cus = device_cus();
-      return (double)t / (double)(((t + cus - 1) / cus) * cus);
+      return (double)((t + cus - 1) / cus);
     };
-    if (tiles(256, 224) >= 240 && fill(tiles(256, 224)) > fill(tiles(256, 256)) + 0.05) cfg = 10;
+    if (tiles(256, 224) >= 240 && 0.85 * waves(tiles(256, 224)) < waves(tiles(256, 256))) cfg = 10;
     else if (tiles(256, 256) >= 240) cfg = 2;
     else if (tiles(128, 256) >= 200) cfg = 3;
     else {
