@@ -1,10 +1,14 @@
 // awq_api.hip -- host side of libcube_awq_gfx950: the reference's launch-time
 // validation, the m_valid / decode-prefill dispatch rule, the module-level
 // tile selection, a per-stream workspace, and the extern "C" ABI of awq.h.
-#include <mutex>
+#include <atomic>
 #include <map>
+#include <mutex>
+#include <set>
 #include <sstream>
+#include <vector>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <utility>
 
@@ -110,25 +114,93 @@ static void validate_decode(const awq_shape_config& s, int64_t g) {
   validate_impl(s, g, kRowsPerThreadDecode, kNLinesPerThreadDecode);
 }
 
-// select_tile_m / select_tile_n, src/modules/awq_gemm.rs:20-52.
+// ---------------------------------------------------------------------------
+// Tuning overrides, read once per process (and by awq_tuning_reload()).
+// ---------------------------------------------------------------------------
+static const char* const kTuneNames[kTuneCount] = {
+    "AWQ_GEMM_TILE",  "AWQ_GEMM_SPLITS", "AWQ_GEMM_GROUP_M", "AWQ_F32_SLICES",  "AWQ_GEMV_WAVES",
+    "AWQ_GEMV_RPW",   "AWQ_MFMA_WAVES",  "AWQ_MFMA_RPW",     "AWQ_M4_WAVES",    "AWQ_M4_RPW",
+    "AWQ_DECODE_MFMA", "AWQ_DECODE_M4",  "AWQ_SMALLM_MFMA",  "AWQ_SKINNY",      "AWQ_SKINNY_SPLITS"};
+static std::atomic<int> g_tune_val[kTuneCount];
+static std::atomic<bool> g_tune_set[kTuneCount];
+static std::once_flag g_tune_once;
+
+// Rust's char::is_whitespace (the Unicode White_Space property), which
+// str::trim strips from both ends.
+static bool rust_whitespace(uint32_t c) {
+  return (c >= 0x09 && c <= 0x0D) || c == 0x20 || c == 0x85 || c == 0xA0 || c == 0x1680 ||
+         (c >= 0x2000 && c <= 0x200A) || c == 0x2028 || c == 0x2029 || c == 0x202F ||
+         c == 0x205F || c == 0x3000;
+}
+
+// Decode UTF-8 (strictly: no overlongs, surrogates or values past U+10FFFF);
+// false for bytes that std::env::var would reject as not Unicode.
+static bool utf8_decode(const char* s, std::vector<uint32_t>& out) {
+  const unsigned char* p = reinterpret_cast<const unsigned char*>(s);
+  while (*p) {
+    uint32_t c = *p, need = 0, min = 0;
+    if (c < 0x80) { need = 0; }
+    else if ((c & 0xE0) == 0xC0) { c &= 0x1F; need = 1; min = 0x80; }
+    else if ((c & 0xF0) == 0xE0) { c &= 0x0F; need = 2; min = 0x800; }
+    else if ((c & 0xF8) == 0xF0) { c &= 0x07; need = 3; min = 0x10000; }
+    else return false;
+    ++p;
+    for (uint32_t i = 0; i < need; ++i, ++p) {
+      if ((*p & 0xC0) != 0x80) return false;
+      c = (c << 6) | (*p & 0x3F);
+    }
+    if (need && c < min) return false;
+    if (c > 0x10FFFF || (c >= 0xD800 && c <= 0xDFFF)) return false;
+    out.push_back(c);
+  }
+  return true;
+}
+
+// AWQ_GEMM_FORCE_TILE_M as the reference reads it (src/modules/awq_gemm.rs:
+// 20-28): std::env::var (absent or not Unicode -> no override), then
+// raw.trim().parse::<usize>() (an optional '+', ASCII digits, no overflow of
+// a 64-bit usize), kept only if it is 8, 16 or 32.
+static int64_t parse_forced_tile_m(const char* raw) {
+  if (!raw) return 0;
+  std::vector<uint32_t> cp;
+  if (!utf8_decode(raw, cp)) return 0;
+  size_t b = 0, e = cp.size();
+  while (b < e && rust_whitespace(cp[b])) ++b;
+  while (e > b && rust_whitespace(cp[e - 1])) --e;
+  if (b < e && cp[b] == '+') ++b;
+  if (b == e) return 0;
+  uint64_t v = 0;
+  for (size_t i = b; i < e; ++i) {
+    if (cp[i] < '0' || cp[i] > '9') return 0;
+    const uint64_t d = cp[i] - '0';
+    if (v > (UINT64_MAX - d) / 10) return 0;  // usize overflow: parse error
+    v = v * 10 + d;
+  }
+  return (v == 8 || v == 16 || v == 32) ? (int64_t)v : 0;
+}
+
+static void tuning_read() {
+  for (int i = 0; i < kTuneCount; ++i) {
+    const char* e = std::getenv(kTuneNames[i]);
+    g_tune_val[i].store(e ? std::atoi(e) : 0, std::memory_order_relaxed);
+    g_tune_set[i].store(e != nullptr, std::memory_order_relaxed);
+  }
+}
+
+int tuning(TuneKey key, int dflt) {
+  std::call_once(g_tune_once, tuning_read);
+  return g_tune_set[key].load(std::memory_order_relaxed) ? g_tune_val[key].load(std::memory_order_relaxed)
+                                                         : dflt;
+}
+
+// Read once per process, like the reference's OnceLock (awq_tuning_reload()
+// does not re-read it).
 static int64_t forced_tile_m() {
-  static const int64_t forced = [] {
-    const char* raw = std::getenv("AWQ_GEMM_FORCE_TILE_M");
-    if (!raw) return (int64_t)0;
-    // Rust: raw.trim().parse::<usize>() then filter {8, 16, 32}.
-    std::string t(raw);
-    size_t b = t.find_first_not_of(" \t\n\r\f\v");
-    size_t e = t.find_last_not_of(" \t\n\r\f\v");
-    if (b == std::string::npos) return (int64_t)0;
-    t = t.substr(b, e - b + 1);
-    if (t.empty() || t.find_first_not_of("0123456789") != std::string::npos) return (int64_t)0;
-    if (t.size() > 6) return (int64_t)0;
-    int64_t v = std::atoll(t.c_str());
-    return (v == 8 || v == 16 || v == 32) ? v : (int64_t)0;
-  }();
+  static const int64_t forced = parse_forced_tile_m(std::getenv("AWQ_GEMM_FORCE_TILE_M"));
   return forced;
 }
 
+// select_tile_m / select_tile_n, src/modules/awq_gemm.rs:20-52.
 static int64_t select_tile_m(int64_t m) {
   if (int64_t f = forced_tile_m()) return f;
   if (m <= kDecodeMThreshold) return kDecodeTileM;
@@ -170,9 +242,12 @@ static void run_gemm(GemmProblem p, int64_t launch_m) {
 }
 
 // ---------------------------------------------------------------------------
-// Workspace: one growable device buffer per (device, stream). Calls on one
+// Workspace: one device buffer per (device, stream, slot). Calls on one
 // stream are ordered, so reuse within a stream is safe; calls on different
-// streams get different buffers.
+// streams get different buffers. A graph captured on a stream keeps the
+// buffers that stream had at capture time, so a buffer is never freed: when
+// a call needs more, a new buffer (at least twice the old size) replaces it
+// for later calls and the old one is retired, alive until the process ends.
 // ---------------------------------------------------------------------------
 struct WsKey {
   int device;
@@ -193,18 +268,34 @@ static std::map<WsKey, WsBuf>& ws_map() {
   static auto* m = new std::map<WsKey, WsBuf>();  // never destroyed: no frees at exit
   return *m;
 }
+static std::vector<void*>& ws_retired() {
+  static auto* v = new std::vector<void*>();  // superseded buffers, kept for captured graphs
+  return *v;
+}
 
 int64_t device_cus() {
-  static int cached[64] = {0};
+  static std::atomic<int> cached[64];
   int dev = 0;
   check_hip(hipGetDevice(&dev), "hipGetDevice");
   if (dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int v = 0;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (!v) {
     check_hip(hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev), "hipDeviceGetAttribute");
-    cached[dev] = v > 0 ? v : 256;
+    if (v <= 0) v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
   }
-  return cached[dev];
+  return v;
+}
+
+void ensure_dyn_smem(const void* kernel, int bytes, const char* what) {
+  static std::mutex mu;
+  static auto* done = new std::set<std::pair<int, const void*>>();
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  std::lock_guard<std::mutex> lk(mu);
+  if (done->count({dev, kernel})) return;
+  check_hip(hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes), what);
+  done->insert({dev, kernel});
 }
 
 void* workspace_get(hipStream_t stream, size_t bytes, int slot) {
@@ -218,20 +309,18 @@ void* workspace_get(hipStream_t stream, size_t bytes, int slot) {
     if (cs != hipStreamCaptureStatusNone)
       panic("the split-K workspace of this stream must be allocated before graph capture: "
             "make one call of the same or a larger shape on this stream outside the capture");
-    if (b.ptr) {
-      // The old buffer may still be in use by work queued on this stream.
-      check_hip(hipStreamSynchronize(stream), "workspace grow: hipStreamSynchronize");
-      check_hip(hipFree(b.ptr), "workspace grow: hipFree");
-      b.ptr = nullptr;
-      b.bytes = 0;
-    }
     size_t want = bytes < (1u << 16) ? (size_t)(1u << 16) : bytes;
+    if (want < 2 * b.bytes) want = 2 * b.bytes;
     want = (want + 4095) & ~(size_t)4095;
-    check_hip(hipMalloc(&b.ptr, want), "workspace hipMalloc");
+    void* fresh = nullptr;
+    check_hip(hipMalloc(&fresh, want), "workspace hipMalloc");
     if (slot == kWsCounters) {
       // Arrival counters must start at zero; every kernel leaves them at zero.
-      check_hip(hipMemsetAsync(b.ptr, 0, want, stream), "workspace hipMemsetAsync");
+      check_hip(hipMemsetAsync(fresh, 0, want, stream), "workspace hipMemsetAsync");
     }
+    // Work already queued (or captured) with the old buffer keeps using it.
+    if (b.ptr) ws_retired().push_back(b.ptr);
+    b.ptr = fresh;
     b.bytes = want;
   }
   return b.ptr;
@@ -412,21 +501,43 @@ int awq_dequantize_native(const awq_tensor_ref* q_weight, const awq_tensor_ref* 
     const int64_t out_width = output->shape[output->rank - 1];
     AWQ_ASSERT(out_width % 32 == 0, "assertion failed: out_width % 32 == 0");
 
-    // Sizes the reference leaves implicit in its linear views: K rows of N/8
-    // words, K/g rows of zeros and scales, a [K, N] output.
-    AWQ_ASSERT(q_weight->rank == 2 && q_zeros->rank == 2 && q_scales->rank == 2 &&
-                   output->rank == 2,
-               "dequantize tensors must be 2-D");
-    const int64_t K = q_weight->shape[0];
+    // The reference reads every tensor through a linear view (any rank) and
+    // runs one unit per 4-word line of q_weight (numel / 4, rounded down):
+    // line i covers output columns 32 (i % (N/32)) .. +31 of row i / (N/32),
+    // whose group is row / group_size; nothing else about the shapes is
+    // asserted. The same lines are computed here. What the reference leaves
+    // unchecked and this library rejects: lines that would read or write past
+    // the end of q_zeros, q_scales or output (out-of-bounds access there),
+    // and group_size or out_width of 0 with work to do (a division by zero).
     const int64_t N = out_width;
-    AWQ_ASSERT(group_size > 0, "group_size must be > 0");
-    AWQ_ASSERT(K % group_size == 0, "k must be divisible by group_size");
-    AWQ_ASSERT_EQ(q_weight->shape[1], N / 8, "qweight packed N must be N/8");
-    AWQ_ASSERT_EQ(q_zeros->shape[0], K / group_size, "qzeros rows must be K/group_size");
-    AWQ_ASSERT_EQ(q_zeros->shape[1], N / 8, "qzeros packed N must be N/8");
-    AWQ_ASSERT_EQ(q_scales->shape[0], K / group_size, "scales rows must be K/group_size");
-    AWQ_ASSERT_EQ(q_scales->shape[1], N, "scales N must match shape.n");
-    AWQ_ASSERT_EQ(output->shape[0], K, "output rows must match qweight rows");
+    const int64_t lines = numel(*q_weight) / 4;
+    if (lines > 0) {
+      AWQ_ASSERT(N > 0, "dequantize: out_width must be > 0 when q_weight is not empty");
+      AWQ_ASSERT(group_size > 0, "group_size must be > 0");
+    }
+    const int64_t lines_per_row = N / 32;
+    const int64_t K = lines_per_row > 0 ? lines / lines_per_row : 0;        // complete rows
+    const int64_t tail_cols = lines_per_row > 0 ? (lines % lines_per_row) * 32 : 0;  // last, partial row
+    if (lines > 0) {
+      // Highest zero word / scale / output element any line touches, + 1.
+      int64_t need_z = 0, need_s = 0;
+      if (K > 0) {
+        const int64_t gl = (K - 1) / group_size;
+        need_z = gl * (N / 8) + N / 8;
+        need_s = gl * N + N;
+      }
+      if (tail_cols > 0) {
+        const int64_t gt = K / group_size;
+        need_z = std::max(need_z, gt * (N / 8) + tail_cols / 8);
+        need_s = std::max(need_s, gt * N + tail_cols);
+      }
+      AWQ_ASSERT(numel(*q_zeros) >= need_z,
+                 "dequantize: q_zeros is too small for q_weight, out_width and group_size");
+      AWQ_ASSERT(numel(*q_scales) >= need_s,
+                 "dequantize: q_scales is too small for q_weight, out_width and group_size");
+      AWQ_ASSERT(numel(*output) >= K * N + tail_cols,
+                 "dequantize: output is too small for q_weight");
+    }
     check_float_dtype(q_scales->dtype, "scales");
     check_float_dtype(output->dtype, "output");
 
@@ -440,13 +551,14 @@ int awq_dequantize_native(const awq_tensor_ref* q_weight, const awq_tensor_ref* 
     p.K = K;
     p.N = N;
     p.group = group_size;
+    p.tail_cols = tail_cols;
     p.order = AWQ_ORDER_SEQUENTIAL;
     p.stream = static_cast<hipStream_t>(stream);
     check_aligned(p.qweight, "qweight");
     check_aligned(p.qzeros, "qzeros");
     check_aligned(p.scales, "scales");
     check_aligned(p.out, "output");
-    if (K > 0 && N > 0) launch_dequant(p);
+    if (lines > 0) launch_dequant(p);
   });
 }
 
@@ -561,6 +673,11 @@ int64_t awq_select_tile_n(int64_t n) { return select_tile_n(n); }
 int64_t awq_decode_m_threshold(void) { return kDecodeMThreshold; }
 
 const char* awq_last_error(void) { return g_last_error.c_str(); }
+
+void awq_tuning_reload(void) {
+  std::call_once(g_tune_once, tuning_read);
+  tuning_read();
+}
 
 int32_t awq_version(void) { return 100; /* 0.1.0 */ }
 

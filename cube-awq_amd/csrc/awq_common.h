@@ -181,7 +181,8 @@ struct DequantProblem {
   int32_t st;
   void* out;
   int32_t ot;
-  int64_t K, N, group;
+  int64_t K, N, group;  // K complete rows of N columns
+  int64_t tail_cols;    // then this many columns (a multiple of 32) of row K
   int32_t order;
   hipStream_t stream;
 };
@@ -201,9 +202,41 @@ void launch_skinny(const GemmProblem& p);
 // Compute units of the current device (queried once per device).
 int64_t device_cus();
 
-// Per-(device, stream, slot) device workspace, grown on demand and never shrunk.
-// kWsCounters is zero-filled when (re)allocated and kernels leave it zero;
-// kWsPartials holds split-K partial sums (contents undefined between calls).
+// Tuning overrides (AWQ_* environment variables that force a route or a
+// launch configuration). They are read from the environment once per process
+// (and again by awq_tuning_reload()), never on the launch path.
+enum TuneKey {
+  kTuneGemmTile,      // AWQ_GEMM_TILE
+  kTuneGemmSplits,    // AWQ_GEMM_SPLITS
+  kTuneGemmGroupM,    // AWQ_GEMM_GROUP_M
+  kTuneF32Slices,     // AWQ_F32_SLICES
+  kTuneGemvWaves,     // AWQ_GEMV_WAVES
+  kTuneGemvRpw,       // AWQ_GEMV_RPW
+  kTuneMfmaWaves,     // AWQ_MFMA_WAVES
+  kTuneMfmaRpw,       // AWQ_MFMA_RPW
+  kTuneM4Waves,       // AWQ_M4_WAVES
+  kTuneM4Rpw,         // AWQ_M4_RPW
+  kTuneDecodeMfma,    // AWQ_DECODE_MFMA
+  kTuneDecodeM4,      // AWQ_DECODE_M4
+  kTuneSmallMMfma,    // AWQ_SMALLM_MFMA
+  kTuneSkinny,        // AWQ_SKINNY
+  kTuneSkinnySplits,  // AWQ_SKINNY_SPLITS
+  kTuneCount
+};
+// The override's value (atoi of the variable), or dflt when it is unset.
+int tuning(TuneKey key, int dflt);
+
+// Opt a kernel in to `bytes` of dynamic LDS on the current device (once per
+// device and kernel; thread-safe).
+void ensure_dyn_smem(const void* kernel, int bytes, const char* what);
+
+// Split-K workspace of a launch: kWsCounters (arrival counters, zero between
+// calls: every kernel that takes one re-arms it) and kWsPartials (fp32
+// partial sums, contents undefined between calls). workspace_get returns a
+// per-(device, stream, slot) library buffer of at least `bytes`; a buffer is
+// never freed once handed out (a graph captured on the stream may still
+// hold it), so growth allocates a new one and retires the old one for the
+// life of the process. Growth is refused during stream capture.
 enum { kWsCounters = 0, kWsPartials = 1 };
 void* workspace_get(hipStream_t stream, size_t bytes, int slot);
 

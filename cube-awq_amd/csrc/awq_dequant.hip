@@ -110,10 +110,12 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint32_t* __restrict
 template <bool kSeq, int ST, int OT>
 void launch_typed(const DequantProblem& p) {
   constexpr int V = 16 / dtype_size_ct(OT);
-  const int R = (p.group % 4 == 0) ? 4 : 1;
+  // 4 rows per item when they always share a group and every item is whole;
+  // a partial last row (tail_cols) is walked one row per item.
+  const int R = (p.group % 4 == 0 && p.K % 4 == 0 && p.tail_cols == 0) ? 4 : 1;
   const uint32_t items_per_row = (uint32_t)(p.N / V);
-  const uint64_t n_items64 = (uint64_t)(p.K / R) * items_per_row;
-  AWQ_ASSERT(n_items64 < (1ull << 32) && (uint64_t)p.K * (uint64_t)p.N < (1ull << 40),
+  const uint64_t n_items64 = (uint64_t)(p.K / R) * items_per_row + (uint64_t)(p.tail_cols / V);
+  AWQ_ASSERT(n_items64 < (1ull << 32) && (uint64_t)(p.K + 1) * (uint64_t)p.N < (1ull << 40),
              "dequantize: tensor too large for one launch");
   const uint32_t n_items = (uint32_t)n_items64;
   if (n_items == 0) return;

@@ -1022,10 +1022,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 // rows by b columns of them (a*b fixed) it fetches a*BM + b*BN/4 row-bytes of
 // X and W per K step (f16 X, 4-bit W), least near a = sqrt(CUs/8 * BN / (4 BM)).
 int raster_group_m(int tiles_m, int bm, int bn) {
-  if (const char* e = std::getenv("AWQ_GEMM_GROUP_M")) {
-    const int v = std::atoi(e);
-    if (v > 0) return std::min(v, tiles_m);
-  }
+  if (const int v = tuning(kTuneGemmGroupM, 0); v > 0) return std::min(v, tiles_m);
   const double conc = (double)std::max<int64_t>(1, device_cus() / 8);
   const double best = std::sqrt(conc * bn / (4.0 * bm));
   int a = 1;
@@ -1067,13 +1064,8 @@ void launch_big_act(const GemmProblem& p, int splits) {
     a.partial = static_cast<float*>(
         workspace_get(p.stream, (size_t)a.splits * p.rows * p.N * sizeof(float), kWsPartials));
   }
-  static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
-  if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT, PP>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)C::kSmem),
-              "hipFuncSetAttribute(gemm_big)");
-    attr_set = true;
-  }
+  ensure_dyn_smem((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT, PP>, (int)C::kSmem,
+                  "hipFuncSetAttribute(gemm_big)");
   hipLaunchKernelGGL((gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT, PP>), dim3(tiles, a.splits),
                      dim3(C::kThreads), C::kSmem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
@@ -1111,13 +1103,8 @@ void launch_cfg_act(const GemmProblem& p) {
   a.swizzled_tiles = tiles & ~7;
   a.splits = 1;
   const size_t smem = C::kSmem;
-  static bool attr_set = false;  // one-time opt-in above 64 KiB of LDS
-  if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ, ACT>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
-              "hipFuncSetAttribute(gemm)");
-    attr_set = true;
-  }
+  ensure_dyn_smem((const void*)gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ, ACT>, (int)smem,
+                  "hipFuncSetAttribute(gemm)");
   hipLaunchKernelGGL((gemm_kernel<MODE, ST, BM, BN, WGM, WGN, SEQ, ACT>), dim3(tiles), dim3(C::kThreads),
                      smem, p.stream, a);
   check_hip(hipGetLastError(), "gemm kernel launch");
@@ -1131,11 +1118,6 @@ void launch_cfg(const GemmProblem& p) {
   launch_cfg_act<MODE, ST, BM, BN, WGM, WGN, SEQ, false>(p);
 }
 
-int env_int(const char* name, int dflt) {
-  const char* e = std::getenv(name);
-  return e ? std::atoi(e) : dflt;
-}
-
 
 // Tile choice. f16/bf16 problems with K % 64 == 0 and group = 64 * 2^j use the
 // large-tile kernel with the largest tile that still yields a full wave of
@@ -1143,7 +1125,7 @@ int env_int(const char* name, int dflt) {
 // 128x128 kernel.
 template <int MODE, int ST, bool SEQ>
 void launch_mode(const GemmProblem& p) {
-  int cfg = env_int("AWQ_GEMM_TILE", 0);  // tuning override: 1 generic, 2.. large tiles
+  int cfg = tuning(kTuneGemmTile, 0);  // tuning override: 1 generic, 2.. large tiles
   const int64_t gs = p.group / kBK;
   const bool big_ok = MODE != MODE_F32 && p.K % kBK == 0 && p.group % kBK == 0 && (gs & (gs - 1)) == 0 &&
                       p.rows * p.K * 2 < (1ll << 32) && p.K * (p.N / 8) * 4 < (1ll << 32) &&
@@ -1232,7 +1214,7 @@ void launch_mode(const GemmProblem& p) {
       }
     }
   }
-  if (int v = env_int("AWQ_GEMM_SPLITS", 0); v >= 1) splits = v;
+  if (int v = tuning(kTuneGemmSplits, 0); v >= 1) splits = v;
   if constexpr (MODE != MODE_F32) {
     switch (cfg) {
       case 2: return launch_big<MODE, ST, 256, 256, 2, 4, 32, SEQ>(p, splits);
@@ -1286,7 +1268,7 @@ void launch_gemm(const GemmProblem& p) {
   // lower (measured 10-35 % faster up to 1024 rows at 4096 -> 14336 and
   // 8192 -> 28672, up to 768 at 14336 -> 4096; slower past 256 at
   // 4096 -> 4096, where the fp32 kernel's time stays flat).
-  const int f32_slices = env_int("AWQ_F32_SLICES", 1);  // 0: never, 2: at any row count
+  const int f32_slices = tuning(kTuneF32Slices, 1);  // 0: never, 2: at any row count
   auto slices_win = [&]() {
     if (p.rows <= 256 || f32_slices == 2) return true;
     if (p.rows > 1024) return false;

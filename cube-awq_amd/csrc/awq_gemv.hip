@@ -16,19 +16,20 @@
 //    Every load a wave needs (its RPW weight words, one x value per lane for
 //    the activation sum, the zero word and the 8 scales) is issued up front,
 //    so a workgroup's whole share of qweight is in flight at once.
-//  * Per wave segment a[m, n] = sum_k x[m, k] * q[k, n] is accumulated and
-//    the zero point and scale folded once:
-//        acc[m, n] += s[g, n] * (a[m, n] - z[g, n] * sum_k x[m, k])
-//    the reference's sum of x * (q - z) * s with one FMA per weight.
-//  * Nibbles reach the FMA without a conversion instruction: AutoAWQ packs
-//    columns (0,1), (2,3), (4,5), (6,7) in packed lanes (0,4), (1,5), (2,6),
-//    (3,7), i.e. in the low nibble of the two 16-bit halves at bit offsets 0,
-//    4, 8, 12. Masking a word with 0x000F000F (or 0x00F000F0, and the same on
-//    the word shifted right by 8) leaves each half holding q (or 16q), which
-//    read as f16 is the exact denormal q * 2^-24; v_fma_mix_f32 widens it and
-//    accumulates x * q * 2^-24 in f32 with the same single rounding as
-//    x * q. Per 8 weights: 1 shift + 4 ands + 8 v_fma_mix_f32. The 2^-24
-//    (2^-20 for the 16q halves) is undone at the end (exact).
+//  * Per wave segment a[m, n] = sum_k x[m, k] * (q[k, n] - z[g, n]) is
+//    accumulated with the exact integer q - z as the weight operand, and the
+//    scale applied once: acc[m, n] += s[g, n] * a[m, n] (the reference's sum
+//    of x * (q - z) * s, one FMA per weight, with no cancellation however
+//    large the mean of x).
+//  * Nibbles reach the FMA as f16 integers without a conversion: AutoAWQ
+//    packs columns (0,1), (2,3), (4,5), (6,7) in packed lanes (0,4), (1,5),
+//    (2,6), (3,7), i.e. in the low nibble of the two 16-bit halves at bit
+//    offsets 0, 4, 8, 12. v_bitop3_b32 keeps one nibble per half and ORs in
+//    an exponent: 0x6400 | q is the f16 1024 + q, 0x5400 | 16q is 64 + q
+//    (mantissa unit 1/16). v_pk_add_f16 of the group's -(1024 + z) (or
+//    -(64 + z)) leaves q - z exactly in both halves, which v_fma_mix_f32
+//    widens and accumulates as x * (q - z) in f32. Per 8 weights: 1 shift +
+//    4 bitop3 + 4 pk_add + 8 v_fma_mix_f32.
 //  * The waves of a workgroup (stacked along K) are summed through LDS in a
 //    fixed order. When K needs more than one workgroup per column chunk
 //    (grid.y = splits), each writes its partial and the last to arrive sums
@@ -101,50 +102,46 @@ __device__ __forceinline__ void scales_to_f32(const RawScales& r, int32_t st, fl
 
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
-// The 4 masked views of a packed word: element j holds columns (2j, 2j+1) as
-// f16 denormals q * 2^-24 (j = 0, 2) or 16q * 2^-24 (j = 1, 3).
-__device__ __forceinline__ void split_word(uint32_t w, uint32_t (&mk)[4]) {
+// The 4 magic views of a packed word: element j holds the two packed lanes
+// of accumulator slots (2j, 2j+1) as f16 1024 + q (j = 0, 2: low nibble of
+// each half) or 64 + q (j = 1, 3: high nibble, mantissa unit 1/16).
+__device__ __forceinline__ void magic_word(uint32_t w, uint32_t (&mk)[4]) {
   const uint32_t w8 = w >> 8;
-  mk[0] = w & 0x000F000Fu;
-  mk[1] = w & 0x00F000F0u;
-  mk[2] = w8 & 0x000F000Fu;
-  mk[3] = w8 & 0x00F000F0u;
+  mk[0] = __builtin_amdgcn_bitop3_b32(w, 0x000F000Fu, 0x64006400u, 0xEA);   // (w & m) | e
+  mk[1] = __builtin_amdgcn_bitop3_b32(w, 0x00F000F0u, 0x54005400u, 0xEA);
+  mk[2] = __builtin_amdgcn_bitop3_b32(w8, 0x000F000Fu, 0x64006400u, 0xEA);
+  mk[3] = __builtin_amdgcn_bitop3_b32(w8, 0x00F000F0u, 0x54005400u, 0xEA);
 }
 
-// acc[c] += x * (scaled q of column c) for the 8 columns of one word.
-__device__ __forceinline__ void fma_word(float (&acc)[8], float x, const uint32_t (&mk)[4]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const h2_t h = __builtin_bit_cast(h2_t, mk[j]);
-    acc[2 * j] = fmaf(x, (float)h[0], acc[2 * j]);          // v_fma_mix_f32, low half
-    acc[2 * j + 1] = fmaf(x, (float)h[1], acc[2 * j + 1]);  // v_fma_mix_f32, high half
-  }
-}
-
-// The same scaled values as plain floats (used for the zero points).
-__device__ __forceinline__ void word_values(uint32_t w, float (&v)[8]) {
+// The negated magic views of a zero word: -(1024 + z) / -(64 + z) per half.
+__device__ __forceinline__ void neg_magic_zero(uint32_t zw, h2_t (&nz)[4]) {
   uint32_t mk[4];
-  split_word(w, mk);
+  magic_word(zw, mk);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const h2_t h = __builtin_bit_cast(h2_t, mk[j]);
-    v[2 * j] = (float)h[0];
-    v[2 * j + 1] = (float)h[1];
-  }
+  for (int j = 0; j < 4; ++j) nz[j] = __builtin_bit_cast(h2_t, mk[j] ^ 0x80008000u);
 }
 
-// Undo the denormal scaling of column c: 2^24 for q halves, 2^20 for 16q halves.
-__device__ __forceinline__ float col_unscale(int c) { return ((c >> 1) & 1) ? 1048576.0f : 16777216.0f; }
+// Exact q - z of the 8 slots of a word, as 4 f16 pairs (v_pk_add_f16: both
+// operands are integers below 2048 of one binade, so the sum is exact).
+__device__ __forceinline__ void qz_word(uint32_t w, const h2_t (&nz)[4], h2_t (&d)[4]) {
+  uint32_t mk[4];
+  magic_word(w, mk);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) d[j] = __builtin_bit_cast(h2_t, mk[j]) + nz[j];
+}
+
+// acc[c] += x * (q - z) of slot c for the 8 slots of one word.
+__device__ __forceinline__ void fma_word(float (&acc)[8], float x, const h2_t (&d)[4]) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    acc[2 * j] = fmaf(x, (float)d[j][0], acc[2 * j]);          // v_fma_mix_f32, low half
+    acc[2 * j + 1] = fmaf(x, (float)d[j][1], acc[2 * j + 1]);  // v_fma_mix_f32, high half
+  }
+}
 
 
 
 constexpr int kCounterStride = 64;  // u32 words between arrival counters (256 B)
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
 
 // ACT (both decode kernels): the gate/up SiLU epilogue (store_out), a template
 // parameter so the plain kernels' code is untouched by it.
@@ -179,23 +176,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
   for (int m = 0; m < MT; ++m) xrow[m] = (int64_t)min(m, rows - 1) * a.K + kc;
 
   // ---- loads, in the order they are consumed (vmcnt retires in issue order) ----
-  // 1. zero word and scales of the group, 2. one x per lane for the activation
-  // sum, 3. the RPW weight words (batches of RB, the next batch requested
-  // before the current one is consumed).
+  // 1. zero word and scales of the group, 2. the RPW weight words (batches of
+  // RB, the next batch requested before the current one is consumed).
   const uint32_t zw = a.qzeros[(int64_t)grp * np + pack_c];
   const RawScales sraw = load_scales_raw(a.scales, a.st, (int64_t)grp * a.N + (int64_t)pack_c * 8);
-  float xl[MT];
-#pragma unroll
-  for (int m = 0; m < MT; ++m) {
-    float v = 0.f;
-#pragma unroll
-    for (int h = 0; h < (RPW + 63) / 64; ++h) {
-      const int r = min(h * 64 + lane, RPW - 1);
-      const float t = load_x<XT>(a.x, xrow[m] + r);
-      v += (h * 64 + lane < RPW) ? t : 0.f;
-    }
-    xl[m] = live ? v : 0.f;
-  }
   constexpr int RB = RPW < 32 ? RPW : 32;
   constexpr int NB = RPW / RB;
   const rsrc_t wr = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
@@ -205,7 +189,9 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
 #pragma unroll
   for (int r = 0; r < RB; ++r) w[0][r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + r) * row_bytes);
 
-  // ---- accumulate sum_k x * q ---------------------------------------------------
+  // ---- accumulate sum_k x * (q - z) ---------------------------------------------
+  h2_t nz[4];
+  neg_magic_zero(zw, nz);
   float part[MT][8];
 #pragma unroll
   for (int m = 0; m < MT; ++m)
@@ -224,8 +210,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
         // Many rows: widen each nibble once (v_cvt_f32_f16 of the same
         // denormal halves, half rate) and reuse it in MT full-rate FMAs,
         // instead of MT half-rate v_fma_mix_f32 per weight.
+        h2_t d[4];
+        qz_word(w[b & 1][r], nz, d);
         float v[8];
-        word_values(w[b & 1][r], v);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) v[c] = (float)d[c >> 1][c & 1];
         // Opaque: otherwise the widening is folded back into v_fma_mix_f32.
 #pragma unroll
         for (int c = 0; c < 8; ++c) asm("" : "+v"(v[c]));
@@ -236,24 +225,23 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
           for (int c = 0; c < 8; ++c) part[m][c] = fmaf(xv, v[c], part[m][c]);
         }
       } else {
-        uint32_t mk[4];
-        split_word(w[b & 1][r], mk);
+        h2_t d[4];
+        qz_word(w[b & 1][r], nz, d);
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
-          fma_word(part[m], load_x<XT>(a.x, xrow[m] + b * RB + r), mk);
+          fma_word(part[m], load_x<XT>(a.x, xrow[m] + b * RB + r), d);
         }
       }
     }
   }
 
-  // ---- fold zero point and scale (zero points in the weights' scaled domain) ----
-  // Accumulator slot c holds the packed lane that split_word puts there: lane
+  // ---- apply the scale -----------------------------------------------------------
+  // Accumulator slot c holds the packed lane that magic_word puts there: lane
   // kAwqLaneOfCol[c], which is column c in AutoAWQ order and column
   // seq_col(c) = (c >> 1) + 4 (c & 1) in sequential order. Zero points come
-  // through the same masks; scales (and, below, outputs) are per column, so in
+  // through the same views; scales (and, below, outputs) are per column, so in
   // sequential order they are permuted to slot order (once per wave).
-  float zl[8], sl[8];
-  word_values(zw, zl);
+  float sl[8];
   scales_to_f32(sraw, a.st, sl);
   const bool seq = a.seq != 0;
   {
@@ -271,10 +259,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
 #pragma unroll
       for (int c = 0; c < 8; ++c) part[m][c] = 0.f;
     }
-    const float xs = wave_sum(xl[m]);  // sum of x over the wave's rows
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
-      acc[m][c] = sl[c] * fmaf(-zl[c], xs, part[m][c]) * col_unscale(c);
+    for (int c = 0; c < 8; ++c) acc[m][c] = sl[c] * part[m][c];
   }
 
   // ---- sum the waves of the workgroup (fixed order) ------------------------------
@@ -860,11 +846,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_m4_kernel(GemvArgs a) {
   finish_chunk<MV, WAVES, WAVES, ACT>(a, red, &s_last, rows, seq);
 }
 
-int env_int(const char* name, int dflt) {
-  const char* e = std::getenv(name);
-  return e ? std::atoi(e) : dflt;
-}
-
 template <int XT, int MT, int WAVES, int RPW>
 void launch_cfg(const GemmProblem& p) {
   const int np = (int)(p.N / 8);
@@ -945,8 +926,8 @@ void launch_rpw(const GemmProblem& p) {
   while (rpw < 128 && 2 * rpw <= rpw_max(XT, MT, waves) && g % (2 * rpw) == 0 &&
          wgs(waves, 2 * rpw) >= 192)
     rpw *= 2;
-  if (int v = env_int("AWQ_GEMV_WAVES", 0); (v == 4 || v == 8 || v == 16) && v <= WMAX) waves = v;
-  if (int v = env_int("AWQ_GEMV_RPW", 0); v >= 4 && g % v == 0) rpw = v;
+  if (int v = tuning(kTuneGemvWaves, 0); (v == 4 || v == 8 || v == 16) && v <= WMAX) waves = v;
+  if (int v = tuning(kTuneGemvRpw, 0); v >= 4 && g % v == 0) rpw = v;
   rpw = cap(waves, rpw);
   while (g % rpw != 0) rpw >>= 1;
 #define AWQ_GEMV_CASE(W, R) \
@@ -1016,8 +997,8 @@ void launch_mfma(const GemmProblem& p) {
   int waves = 8;
   if (rpw == 64 && wgs(8, 64) < 192) rpw = 32;
   if (rpw == 64 && MV <= 4 && wgs(8, 64) >= 2 * device_cus()) rpw = 32;
-  if (int v = env_int("AWQ_MFMA_WAVES", 0); v == 4 || v == 8) waves = v;
-  if (int v = env_int("AWQ_MFMA_RPW", 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
+  if (int v = tuning(kTuneMfmaWaves, 0); v == 4 || v == 8) waves = v;
+  if (int v = tuning(kTuneMfmaRpw, 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
   if (waves == 8 && rpw == 64) return launch_mfma_cfg<XT, MV, 8, 64>(p);
   if (waves == 8) return launch_mfma_cfg<XT, MV, 8, 32>(p);
   if (rpw == 64) return launch_mfma_cfg<XT, MV, 4, 64>(p);
@@ -1074,8 +1055,8 @@ void launch_m4(const GemmProblem& p) {
   const int64_t wgs64 = chunks * ((p.K + 511) / 512);
   int waves = k16 ? 16 : 8;
   int rpw = (!k16 && p.group % 64 == 0 && wgs64 >= 192 && wgs64 < 512) ? 64 : 32;
-  if (int v = env_int("AWQ_M4_WAVES", 0); v == 8 || (v == 16 && k16)) waves = v;
-  if (int v = env_int("AWQ_M4_RPW", 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
+  if (int v = tuning(kTuneM4Waves, 0); v == 8 || (v == 16 && k16)) waves = v;
+  if (int v = tuning(kTuneM4Rpw, 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
   if constexpr (k16) {
     if (waves == 16) return launch_m4_cfg<XT, MV, 16, 32>(p);
   }
@@ -1090,7 +1071,7 @@ void launch_xt(const GemmProblem& p) {
   // kernel with 16 waves measured faster (4096 x 4096 / 4096 x 1024 /
   // 8192 x 1024: 8.4 / 8.4 / 10.3 us against 10.5 / 10.2 / 11.7).
   // AWQ_DECODE_MFMA=0/1 forces the choice.
-  const int force = env_int("AWQ_DECODE_MFMA", -1);
+  const int force = tuning(kTuneDecodeMfma, -1);
   const bool small2 = p.rows == 2 && p.K * p.N <= 4096ll * 4096ll;
   const bool mfma_ok = p.rows >= 2 && p.group % 32 == 0 && p.K % 32 == 0 &&
                        (force == 1 || (force != 0 && !small2));
@@ -1100,7 +1081,7 @@ void launch_xt(const GemmProblem& p) {
   // 14.6 with f32; 5..8 rows stay on the 16x16x32 kernel (at 8 rows the
   // 4x4x4 MFMAs, twice as many, measured 5-45 % slower). AWQ_DECODE_M4=0
   // forces the 16x16x32 kernel.
-  if (mfma_ok && p.rows <= 4 && env_int("AWQ_DECODE_M4", 1) != 0) return launch_m4<XT, 4>(p);
+  if (mfma_ok && p.rows <= 4 && tuning(kTuneDecodeM4, 1) != 0) return launch_m4<XT, 4>(p);
   if (mfma_ok) {
     // Rows kept in LDS, the workspace and the final reduction (the MFMA
     // tile always computes 16).
@@ -1121,7 +1102,7 @@ void launch_xt(const GemmProblem& p) {
 // outputs it suits). AWQ_SMALLM_MFMA=0 sends them to the prefill kernels.
 bool small_m_mfma_ok(const GemmProblem& p, int64_t launch_m) {
   return launch_m > 8 && launch_m <= 16 && p.rows <= 16 && p.group % 32 == 0 && p.K % 32 == 0 &&
-         env_int("AWQ_SMALLM_MFMA", 1) != 0 && !skinny_ok(p);
+         tuning(kTuneSmallMMfma, 1) != 0 && !skinny_ok(p);
 }
 
 void launch_gemv(const GemmProblem& p) {

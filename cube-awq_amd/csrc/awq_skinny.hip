@@ -447,11 +447,6 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   }
 }
 
-int env_int(const char* name, int dflt) {
-  const char* e = std::getenv(name);
-  return e ? std::atoi(e) : dflt;
-}
-
 template <int MT, bool BF>
 void launch_mt(const GemmProblem& p) {
   constexpr int kXSlot = 16 * MT * 64;
@@ -469,7 +464,7 @@ void launch_mt(const GemmProblem& p) {
   splits = std::min(splits, std::max(1, total_steps / 16));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (8 * p.rows)));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, 1024 / p.rows));
-  if (int v = env_int("AWQ_SKINNY_SPLITS", 0); v >= 1) splits = std::min(v, total_steps);
+  if (int v = tuning(kTuneSkinnySplits, 0); v >= 1) splits = std::min(v, total_steps);
   int sps = (total_steps + splits - 1) / splits;
   while ((int64_t)sps * kStep / p.group + 2 > kMaxGroups) {
     ++splits;
@@ -504,16 +499,8 @@ void launch_mt(const GemmProblem& p) {
     a.partial = static_cast<float*>(
         workspace_get(p.stream, (size_t)splits * p.rows * p.N * sizeof(float), kWsPartials));
   }
-  static bool attr_set = false;
-  if (!attr_set) {
-    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, false, BF>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
-              "hipFuncSetAttribute(skinny)");
-    check_hip(hipFuncSetAttribute((const void*)skinny_kernel<MT, true, BF>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem),
-              "hipFuncSetAttribute(skinny)");
-    attr_set = true;
-  }
+  ensure_dyn_smem((const void*)skinny_kernel<MT, false, BF>, (int)smem, "hipFuncSetAttribute(skinny)");
+  ensure_dyn_smem((const void*)skinny_kernel<MT, true, BF>, (int)smem, "hipFuncSetAttribute(skinny)");
   if (p.act)
     hipLaunchKernelGGL((skinny_kernel<MT, true, BF>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
   else
@@ -540,7 +527,7 @@ bool skinny_ok(const GemmProblem& p) {
   // with K >= 8192. 9..16 rows of f16/bf16 also come here instead of the
   // decode kernels' 16-row tile (f16 0-28 % faster at K 4096..28672,
   // N 1024..28672; bf16 -8..+20 %). AWQ_SKINNY=0/1 forces the choice.
-  const int force = env_int("AWQ_SKINNY", -1);
+  const int force = tuning(kTuneSkinny, -1);
   const bool wins = p.N >= 6144 || (p.N >= 1024 && (p.rows <= 32 || (p.rows <= 64 && p.K >= 8192)));
   if (force == 0 || (force != 1 && !wins)) return false;
   // bf16 activations need 16-bit scales (z s exact in f32, see the kernel).

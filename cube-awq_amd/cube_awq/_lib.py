@@ -70,6 +70,7 @@ SIGNATURES = {
     "awq_select_tile_m": (ctypes.c_int64, [_I64]),
     "awq_select_tile_n": (ctypes.c_int64, [_I64]),
     "awq_decode_m_threshold": (ctypes.c_int64, []),
+    "awq_tuning_reload": (None, []),
     "awq_last_error": (ctypes.c_char_p, []),
     "awq_version": (ctypes.c_int32, []),
 }

@@ -5,9 +5,24 @@
  * Every pointer named qweight/qzeros/scales/x/y/out/bias is a DEVICE pointer to
  * caller-owned, row-major, contiguous memory. Calls are stream-ordered and
  * asynchronous: they enqueue work on `stream` (a hipStream_t passed as void*,
- * NULL = the legacy default stream) and never synchronise the host. No call
- * allocates device memory except the GEMM split-K workspace described at
- * awq_gemm_linear(), which is allocated once per (device, stream) and reused.
+ * NULL = the legacy default stream) and never synchronise the host.
+ *
+ * Workspace. The GEMM entry points allocate device memory in one case: a
+ * launch that splits K over several workgroups keeps fp32 partial sums
+ * (splits x rows x N x 4 bytes) and arrival counters (<= 256 bytes per
+ * column chunk or tile) in a workspace owned by the library, one per
+ * (device, stream). Routes that split K: the decode kernels (M <= 16) when K
+ * spans more than one workgroup's rows, the 17..128-row kernel, the
+ * large-tile kernel when it has few tiles (about M <= 1024), and fp32
+ * activations run as 16-row slices. The workspace is allocated on first need
+ * and grown when a call needs more; a superseded buffer is never freed (it is
+ * retired and kept until the process ends), so work queued or captured
+ * earlier stays valid. Growth during stream capture is refused with an
+ * error: before capturing, make one eager call on the capture stream with
+ * the largest shape the graph will hold. A graph keeps the workspace its
+ * capture stream had: replays of graphs captured on one stream, and eager
+ * calls on that stream, share it and must not overlap in time (replay them
+ * on the capture stream, or order them with events).
  *
  * Return value: 0 on success, a negative AWQ_ERR_* code otherwise. On error the
  * thread-local string returned by awq_last_error() holds the message; for shape
@@ -165,6 +180,14 @@ int64_t awq_select_tile_n(int64_t n);
 
 /* DECODE_M_THRESHOLD (src/kernel/awq_kernel_gemm.rs:81): M <= this runs the GEMV. */
 int64_t awq_decode_m_threshold(void);
+
+/* Re-read the AWQ_* tuning overrides (environment variables that force a
+ * kernel route or launch configuration, used by tests and tuning sweeps).
+ * The library reads them once per process, on its first launch, so that no
+ * launch pays for a getenv(); call this after changing one. No reference
+ * counterpart (the reference has no such overrides besides
+ * AWQ_GEMM_FORCE_TILE_M, which, as there, is read once and not re-read). */
+void awq_tuning_reload(void);
 
 /* Thread-local message of the last failing call on this thread ("" if none). */
 const char* awq_last_error(void);

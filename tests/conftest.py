@@ -29,3 +29,34 @@ def dev():
     import cube_awq
     cube_awq.lib()  # fail loudly if the HIP library is not built
     return torch.device("cuda:0")
+
+
+@pytest.fixture(autouse=True)
+def _tuning_overrides(monkeypatch):
+    """The library reads its AWQ_* tuning overrides once per process
+    (awq_tuning_reload() re-reads them): re-read them whenever a test sets
+    one, and again once the test's environment has been restored."""
+    real_setenv, real_delenv = monkeypatch.setenv, monkeypatch.delenv
+    touched = []
+
+    def reload():
+        import cube_awq
+        cube_awq.lib().awq_tuning_reload()
+
+    def setenv(name, value, prepend=None):
+        real_setenv(name, value, prepend)
+        if name.startswith("AWQ_"):
+            touched.append(name)
+            reload()
+
+    def delenv(name, raising=True):
+        real_delenv(name, raising)
+        if name.startswith("AWQ_"):
+            touched.append(name)
+            reload()
+
+    monkeypatch.setenv, monkeypatch.delenv = setenv, delenv
+    yield
+    if touched:
+        monkeypatch.undo()
+        reload()

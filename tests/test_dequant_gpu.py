@@ -108,3 +108,59 @@ def test_linear_forward_matches_cpu_matmul(dev):
     expect = x.double() @ torch.from_numpy(g["expected"]).double()
     assert tuple(y.shape) == (2, 32)
     assert (y.cpu().double() - expect).abs().max().item() <= 1e-3
+
+
+def _native(qw, qz, sc, out, g, dev):
+    cube_awq.dequantize_native(torch.from_numpy(np.ascontiguousarray(qw).view(np.int32)).to(dev),
+                               torch.from_numpy(np.ascontiguousarray(qz).view(np.int32)).to(dev),
+                               torch.from_numpy(np.ascontiguousarray(sc)).to(dev), out, g)
+    torch.cuda.synchronize()
+    return to_host(out)
+
+
+def test_dequantize_native_any_rank(dev):
+    # The reference reads every tensor through a linear view
+    # (src/kernel/awq_kernel.rs:89-106): a [2, K/2, N/8] q_weight with a
+    # [2, K/2, N] output is the same computation as the 2-D one.
+    K, N, g = 256, 128, 64
+    _, qw, qz, sc, _ = make_problem(1, K, N, g, s_dt="f32", scale_range=(-0.03, 0.03))
+    flat = _native(qw, qz, sc, torch.full((K, N), float("nan"), device=dev), g, dev)
+    got = _native(qw.reshape(2, K // 2, N // 8), qz.reshape(1, K // g, N // 8), sc.reshape(K // g, 1, N),
+                  torch.full((2, K // 2, N), float("nan"), device=dev), g, dev)
+    ref = oracle.dequant(qw, qz, sc, g, "seq")
+    assert np.array_equal(flat.view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(got.reshape(K, N).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("K,g", [(96, 64), (200, 128), (130, 4), (66, 64)])
+def test_dequantize_native_partial_last_group(dev, K, g):
+    # K % group_size != 0: the reference asserts nothing about it and the last
+    # group (row / group_size) is simply shorter.
+    N = 64
+    groups = -(-K // g)
+    rng = np.random.default_rng(K + g)
+    qw = rng.integers(0, 2 ** 32, size=(K, N // 8), dtype=np.uint64).astype(np.uint32)
+    qz = rng.integers(0, 2 ** 32, size=(groups, N // 8), dtype=np.uint64).astype(np.uint32)
+    sc = rng.uniform(-0.03, 0.03, size=(groups, N)).astype(np.float32)
+    got = _native(qw, qz, sc, torch.full((K, N), float("nan"), device=dev), g, dev)
+    assert np.array_equal(got.view(np.uint32), oracle.dequant(qw, qz, sc, g, "seq").view(np.uint32))
+
+
+@pytest.mark.parametrize("extra_lines,extra_words", [(1, 0), (3, 0), (2, 3), (0, 2)])
+def test_dequantize_native_ragged_q_weight(dev, extra_lines, extra_words):
+    # One unit per 4-word line of q_weight (numel / 4, rounded down): extra
+    # lines fill the first 32 * extra_lines columns of one more output row;
+    # 1..3 trailing words past the last whole line are ignored.
+    K, N, g = 64, 256, 32
+    rng = np.random.default_rng(11 + extra_lines)
+    qw = rng.integers(0, 2 ** 32, size=((K + 1), N // 8), dtype=np.uint64).astype(np.uint32)
+    qz = rng.integers(0, 2 ** 32, size=(K // g + 1, N // 8), dtype=np.uint64).astype(np.uint32)
+    sc = rng.uniform(-0.03, 0.03, size=(K // g + 1, N)).astype(np.float32)
+    words = K * N // 8 + 4 * extra_lines + extra_words
+    n_out = K * N + 32 * extra_lines
+    # out_width is the output's last dim; row K past the extra lines must stay NaN.
+    out = torch.full((K + 1, N), float("nan"), device=dev)
+    got = _native(qw.reshape(-1)[:words], qz, sc, out, g, dev).reshape(-1)
+    ref = oracle.dequant(qw, qz, sc, g, "seq").reshape(-1)[:n_out]
+    assert np.array_equal(got[:n_out].view(np.uint32), ref.view(np.uint32))
+    assert np.isnan(got[n_out:]).all()

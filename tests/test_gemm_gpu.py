@@ -204,9 +204,12 @@ def test_prefill_sweep_f16(dev, M, K, N):
     assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, None, 128, "f16", "f16")) <= TOL_MFMA
 
 
-def test_prefill_m2048_gate_up_sampled_rows(dev):
-    # Full-size prefill (M=2048, 4096 -> 14336): checked on 48 sampled rows.
-    M, K, N, g = 2048, 4096, 14336, 128
+@pytest.mark.parametrize("K,N", [(4096, 14336), (4096, 4096), (14336, 4096)])
+def test_prefill_m2048_sampled_rows(dev, K, N):
+    # Full-size prefill at M=2048 on the three Llama-3-8B shapes (256 x 224
+    # ping-pong tiles for 4096 -> 14336, 128 x 256 tiles with K up to 14336
+    # for the others): checked on 48 sampled rows.
+    M, g = 2048, 128
     x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f16", s_dt="f16")
     y = _gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f16", "f16", "f16")
     rows = np.r_[0:16, 1000:1016, 2032:2048]
@@ -442,16 +445,21 @@ def test_decode_m4_edge_shapes(dev, monkeypatch, K, N, g, x_dt, M):
 
 
 @pytest.mark.parametrize("row_scales", [(1e6, 1e-6, 1.0, 3e4), (1e30, 1e-30, 7e4, 1e-20), (65504.0, 1e5, 2e-8, 1.0)])
-@pytest.mark.parametrize("kernel", ["m4", "mfma16"])
+@pytest.mark.parametrize("kernel", ["m4", "mfma16", "valu", "valu_m1"])
 def test_decode_mfma_activation_magnitudes(dev, monkeypatch, row_scales, kernel):
     """fp32 activations far outside the f16 range, and far below it, in
-    different rows of one call: each output row keeps fp32 accuracy."""
-    for k, v in DECODE_KERNELS[kernel].items():
+    different rows of one call (valu_m1: one M = 1 call per row, the
+    headline decode kernel): each output row keeps fp32 accuracy."""
+    for k, v in DECODE_KERNELS.get(kernel, {}).items():
         monkeypatch.setenv(k, v)
     M, K, N, g = 4, 1024, 1024, 128
     x, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt="f32", s_dt="f16")
     x = (x * np.asarray(row_scales, dtype=np.float64)[:, None]).astype(np.float32)
-    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f32", "f16", "f32"))
+    if kernel == "valu_m1":
+        y = np.concatenate([to_host(_gemm_ptr(dev, x[m:m + 1], qw, qz, sc, None, 1, K, N, g, "f32", "f16",
+                                              "f32")) for m in range(M)])
+    else:
+        y = to_host(_gemm_ptr(dev, x, qw, qz, sc, None, M, K, N, g, "f32", "f16", "f32"))
     ref = _ref64(x, qw, qz, sc, None, g, "f32", "f16")
     for m in range(M):
         assert np.isfinite(y[m]).all()

@@ -341,3 +341,61 @@ def test_interleave_packed_round_trip():
     t = pack.interleave_packed(torch.from_numpy(pack.pack(a, "awq").view(np.int32)),
                                torch.from_numpy(pack.pack(b, "awq").view(np.int32)))
     assert t.dtype == torch.int32 and np.array_equal(t.numpy().view(np.uint32), w)
+
+
+@pytest.mark.parametrize("qz_rows,sc_rows,out_rows,msg", [
+    (1, 2, 96, "q_zeros is too small"), (2, 1, 96, "q_scales is too small"),
+    (2, 2, 95, "output is too small")])
+def test_dequantize_native_rejects_out_of_bounds(qz_rows, sc_rows, out_rows, msg):
+    # K = 96 rows, g = 64 -> groups 0 and 1. The reference reads these through
+    # unchecked linear views; here a buffer too small to hold what the lines of
+    # q_weight touch is rejected before any launch.
+    with pytest.raises(Panic, match=msg):
+        cube_awq.dequantize_native(torch.zeros(96, 4, dtype=torch.int32),
+                                   torch.zeros(qz_rows, 4, dtype=torch.int32),
+                                   torch.ones(sc_rows, 32), torch.zeros(out_rows, 32), 64)
+
+
+def test_dequantize_native_rejects_division_by_zero():
+    with pytest.raises(Panic, match="group_size must be > 0"):
+        cube_awq.dequantize_native(torch.zeros(8, 4, dtype=torch.int32), torch.zeros(1, 4, dtype=torch.int32),
+                                   torch.ones(1, 32), torch.zeros(8, 32), 0)
+    with pytest.raises(Panic, match="out_width must be > 0"):
+        cube_awq.dequantize_native(torch.zeros(8, 4, dtype=torch.int32), torch.zeros(1, 4, dtype=torch.int32),
+                                   torch.ones(1, 32), torch.zeros(8, 0), 64)
+
+
+def test_dequantize_native_empty_q_weight_is_a_no_op():
+    # No lines, no work: accepted whatever the other sizes (as in the reference).
+    cube_awq.dequantize_native(torch.zeros(0, 4, dtype=torch.int32), torch.zeros(0, 4, dtype=torch.int32),
+                               torch.ones(0, 32), torch.zeros(0, 32), 0)
+
+
+# AWQ_GEMM_FORCE_TILE_M is read the way the reference reads it
+# (src/modules/awq_gemm.rs:20-28): std::env::var (absent or not Unicode ->
+# no override), raw.trim() (Unicode White_Space), parse::<usize>() (optional
+# '+', ASCII digits, no 64-bit overflow), kept if 8, 16 or 32. Read once per
+# process (a OnceLock there), so each case runs in its own process.
+_FORCE_CASES = [
+    (b"16", 16), (b"+16", 16), (b"0000016", 16), (b"  32\t", 32), (b"\n8\r\n", 8),
+    ("\u300016\u00a0".encode(), 16), ("16\u2028".encode(), 16), ("\u0085\u2003" "8\u3000".encode(), 8),
+    (b"00000000000000000000000000000032", 32),
+    (b"++16", None), (b"1 6", None), (b"\x1c16", None), (b"-16", None), (b"64", None), (b"", None),
+    (b"+", None), (b"0x10", None), (b"18446744073709551616", None), (b"\xff16", None), (b"16.0", None),
+    ("\u200b16".encode(), None)]
+
+
+@pytest.mark.parametrize("raw,forced", _FORCE_CASES)
+def test_forced_tile_m_parses_like_rust(raw, forced):
+    import os
+    import subprocess
+    import sys
+    from cube_awq import _lib as lib_mod
+    code = ("import ctypes, sys; L = ctypes.CDLL(sys.argv[1]); "
+            "L.awq_select_tile_m.restype = ctypes.c_int64; "
+            "L.awq_select_tile_m.argtypes = [ctypes.c_int64]; print(L.awq_select_tile_m(100))")
+    env = {k: v for k, v in os.environb.items() if k != b"AWQ_GEMM_FORCE_TILE_M"}
+    env[b"AWQ_GEMM_FORCE_TILE_M"] = raw
+    out = subprocess.run([sys.executable, "-c", code, lib_mod.LIB_PATH], env=env, check=True,
+                         capture_output=True).stdout
+    assert int(out) == (forced if forced is not None else 32), raw
