@@ -326,6 +326,56 @@ void* workspace_get(hipStream_t stream, size_t bytes, int slot) {
   return b.ptr;
 }
 
+// ---------------------------------------------------------------------------
+// Static split-K scratch of awq_gemm_noalloc: a file-scope device array,
+// one copy per GPU, held for the life of the process. The first 1 MiB holds
+// arrival counters (zero between calls: every split-K kernel re-arms the
+// counters it uses), the rest fp32 partial sums. Host code never names the
+// array itself (its host-side name is not a device address): its address on
+// each device comes from hipGetSymbolAddress, looked up once per device on
+// the first awq_gemm_noalloc call there, which also clears the counters with
+// a fill kernel on the caller's stream.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchCounterBytes = size_t(1) << 20;
+constexpr size_t kScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void fill_zero_u32(uint32_t* p, uint32_t n) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+static void* scratch_on_device(hipStream_t stream) {
+  static std::mutex mu;
+  static void* ptrs[64] = {};
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) panic("awq_gemm_noalloc: device index out of range (0..63)");
+  std::lock_guard<std::mutex> lk(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    check_hip(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "awq_gemm_noalloc: hipGetSymbolAddress(scratch)");
+    if (!ptr) panic("awq_gemm_noalloc: hipGetSymbolAddress(scratch) returned null");
+    const uint32_t words = (uint32_t)(kScratchCounterBytes / 4);
+    hipLaunchKernelGGL(fill_zero_u32, dim3(256), dim3(256), 0, stream, static_cast<uint32_t*>(ptr), words);
+    check_hip(hipGetLastError(), "awq_gemm_noalloc: clearing the scratch counters");
+    ptrs[dev] = ptr;
+  }
+  return ptrs[dev];
+}
+
+void* ws_get(const GemmProblem& p, size_t bytes, int slot) {
+  if (!p.scratch) return workspace_get(p.stream, bytes, slot);
+  const size_t cap = slot == kWsCounters ? kScratchCounterBytes : kScratchBytes - kScratchCounterBytes;
+  if (bytes > cap) {
+    std::ostringstream os;
+    os << "awq_gemm_noalloc: this call needs " << bytes << " bytes of split-K "
+       << (slot == kWsCounters ? "counters" : "partial sums") << ", more than the " << cap
+       << " bytes of the static scratch (awq_gemm has no such limit)";
+    panic(os.str());
+  }
+  return static_cast<char*>(p.scratch) + (slot == kWsCounters ? 0 : kScratchCounterBytes);
+}
+
 static int64_t numel(const awq_tensor_ref& t) {
   int64_t n = 1;
   for (int i = 0; i < t.rank; ++i) n *= t.shape[i];
@@ -567,7 +617,7 @@ int awq_dequantize_native(const awq_tensor_ref* q_weight, const awq_tensor_ref* 
 static int gemm_entry(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
                       const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
                       int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
-                      int32_t order, int32_t act, void* stream) {
+                      int32_t order, int32_t act, void* stream, bool noalloc = false) {
   return guarded([&] {
     AWQ_ASSERT(M >= 0 && K >= 0 && N >= 0, "shape sizes must be non-negative");
     awq_shape_config s = awq_shape_config_new(M, N, K, select_tile_m(M), select_tile_n(N), kInnerK);
@@ -600,6 +650,7 @@ static int gemm_entry(const void* x, int32_t x_t, const uint32_t* qweight, const
     p.order = order;
     p.act = act;
     p.stream = static_cast<hipStream_t>(stream);
+    if (noalloc && M > 0 && N > 0) p.scratch = scratch_on_device(p.stream);
     run_gemm(p, M);
   });
 }
@@ -609,6 +660,13 @@ int awq_gemm(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t
              int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream) {
   return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
                     AWQ_ORDER_AUTOAWQ, 0, stream);
+}
+
+int awq_gemm_noalloc(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                     const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                     int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size, void* stream) {
+  return gemm_entry(x, x_t, qweight, qzeros, scales, s_t, bias, b_t, y, y_t, M, K, N, group_size,
+                    AWQ_ORDER_AUTOAWQ, 0, stream, true);
 }
 
 int awq_gemm_silu_mul(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,

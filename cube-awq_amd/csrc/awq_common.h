@@ -172,6 +172,7 @@ struct GemmProblem {
   int32_t order;  // AWQ_ORDER_AUTOAWQ (awq_gemm) or AWQ_ORDER_SEQUENTIAL (AWQLinear's weights)
   int32_t act;    // 1: gate/up interleaved by column, y [rows, N/2] = SiLU(gate) * up
   hipStream_t stream;
+  void* scratch;  // static split-K scratch (awq_gemm_noalloc), or null: library workspace
 };
 
 struct DequantProblem {
@@ -239,5 +240,9 @@ void ensure_dyn_smem(const void* kernel, int bytes, const char* what);
 // life of the process. Growth is refused during stream capture.
 enum { kWsCounters = 0, kWsPartials = 1 };
 void* workspace_get(hipStream_t stream, size_t bytes, int slot);
+// The split-K buffer of one launch of problem p: a region of p.scratch when
+// it is set (awq_gemm_noalloc; sizes past the region are an error, nothing is
+// allocated), else workspace_get on p.stream.
+void* ws_get(const GemmProblem& p, size_t bytes, int slot);
 
 }  // namespace cube_awq

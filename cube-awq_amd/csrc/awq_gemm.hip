@@ -1060,9 +1060,9 @@ void launch_big_act(const GemmProblem& p, int splits) {
   a.splits = (total_stages + a.stages_per_split - 1) / a.stages_per_split;  // no empty split
   if (a.splits > 1) {
     a.counters = static_cast<uint32_t*>(
-        workspace_get(p.stream, (size_t)tiles * kTileCtrStride * sizeof(uint32_t), kWsCounters));
+        ws_get(p, (size_t)tiles * kTileCtrStride * sizeof(uint32_t), kWsCounters));
     a.partial = static_cast<float*>(
-        workspace_get(p.stream, (size_t)a.splits * p.rows * p.N * sizeof(float), kWsPartials));
+        ws_get(p, (size_t)a.splits * p.rows * p.N * sizeof(float), kWsPartials));
   }
   ensure_dyn_smem((const void*)gemm_big_kernel<MODE, ST, BM, BN, WGM, WGN, MS, SEQ, ACT, PP>, (int)C::kSmem,
                   "hipFuncSetAttribute(gemm_big)");

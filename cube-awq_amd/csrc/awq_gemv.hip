@@ -872,8 +872,8 @@ void launch_cfg(const GemmProblem& p) {
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MT * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
-    a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
-    a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
+    a.counters = static_cast<uint32_t*>(ws_get(p, ctr_bytes, kWsCounters));
+    a.partial = static_cast<float*>(ws_get(p, part_bytes, kWsPartials));
   }
   if (p.act)
     hipLaunchKernelGGL((gemv_kernel<XT, MT, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES), 0,
@@ -967,8 +967,8 @@ void launch_mfma_cfg(const GemmProblem& p) {
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
-    a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
-    a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
+    a.counters = static_cast<uint32_t*>(ws_get(p, ctr_bytes, kWsCounters));
+    a.partial = static_cast<float*>(ws_get(p, part_bytes, kWsPartials));
   }
   if (p.act)
     hipLaunchKernelGGL((gemv_mfma_kernel<XT, MV, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES),
@@ -1029,8 +1029,8 @@ void launch_m4_cfg(const GemmProblem& p) {
   if (splits > 1) {
     const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
     const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
-    a.counters = static_cast<uint32_t*>(workspace_get(p.stream, ctr_bytes, kWsCounters));
-    a.partial = static_cast<float*>(workspace_get(p.stream, part_bytes, kWsPartials));
+    a.counters = static_cast<uint32_t*>(ws_get(p, ctr_bytes, kWsCounters));
+    a.partial = static_cast<float*>(ws_get(p, part_bytes, kWsPartials));
   }
   if (p.act)
     hipLaunchKernelGGL((gemv_m4_kernel<XT, MV, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES), 0,

@@ -495,9 +495,9 @@ void launch_mt(const GemmProblem& p) {
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
   if (splits > 1) {
     a.counters = static_cast<uint32_t*>(
-        workspace_get(p.stream, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));
+        ws_get(p, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));
     a.partial = static_cast<float*>(
-        workspace_get(p.stream, (size_t)splits * p.rows * p.N * sizeof(float), kWsPartials));
+        ws_get(p, (size_t)splits * p.rows * p.N * sizeof(float), kWsPartials));
   }
   ensure_dyn_smem((const void*)skinny_kernel<MT, false, BF>, (int)smem, "hipFuncSetAttribute(skinny)");
   ensure_dyn_smem((const void*)skinny_kernel<MT, true, BF>, (int)smem, "hipFuncSetAttribute(skinny)");

@@ -65,6 +65,8 @@ SIGNATURES = {
     "awq_validate_gemm": (ctypes.c_int, [_I64, _I64, _I64, _I64]),
     "awq_gemm_ordered": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _P, _I32, _P, _I32,
                                         _I64, _I64, _I64, _I64, _I32, _P]),
+    "awq_gemm_noalloc": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _P, _I32, _P, _I32,
+                                        _I64, _I64, _I64, _I64, _P]),
     "awq_gemm_silu_mul": (ctypes.c_int, [_P, _I32, _P, _P, _P, _I32, _P, _I32, _P, _I32,
                                          _I64, _I64, _I64, _I64, _P]),
     "awq_select_tile_m": (ctypes.c_int64, [_I64]),

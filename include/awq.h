@@ -146,6 +146,26 @@ int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const 
                      int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
                      int32_t order, void* stream);
 
+/* awq_gemm without any device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, serving loops and harnesses that forbid
+ * hipMalloc). No counterpart in the reference (whose launcher allocates
+ * nothing because it never splits K). Same arguments, constraints, kernels
+ * and results as awq_gemm; split-K partial sums and arrival counters go to
+ * a static scratch array in device memory (64 MiB per GPU: 1 MiB of
+ * counters, 63 MiB of fp32 partials, held by every GPU the library runs on
+ * until the process ends) instead of the per-stream workspace. A call whose
+ * route needs more partials than that (splits x rows x N x 4 bytes) fails
+ * with AWQ_ERR_INVALID before launching anything. The first call on a
+ * device looks the array up (hipGetSymbolAddress) and clears its counters
+ * with a kernel on `stream`: make that call outside graph capture. Every
+ * call on one GPU shares that GPU's scratch: calls that overlap in time on
+ * one GPU (other streams, concurrent graph replays) race and must be
+ * serialised by the caller. */
+int awq_gemm_noalloc(const void* x, int32_t x_t, const uint32_t* qweight, const uint32_t* qzeros,
+                     const void* scales, int32_t s_t, const void* bias, int32_t b_t, void* y,
+                     int32_t y_t, int64_t M, int64_t K, int64_t N, int64_t group_size,
+                     void* stream);
+
 /* Fused gate/up projection with its activation in the GEMM epilogue: the
  * weights hold the gate and up projections interleaved by column (column 2j
  * of qweight/qzeros/scales/bias is gate column j, column 2j + 1 is up column
