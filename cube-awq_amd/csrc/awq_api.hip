@@ -120,7 +120,8 @@ static void validate_decode(const awq_shape_config& s, int64_t g) {
 static const char* const kTuneNames[kTuneCount] = {
     "AWQ_GEMM_TILE",  "AWQ_GEMM_SPLITS", "AWQ_GEMM_GROUP_M", "AWQ_F32_SLICES",  "AWQ_GEMV_WAVES",
     "AWQ_GEMV_RPW",   "AWQ_MFMA_WAVES",  "AWQ_MFMA_RPW",     "AWQ_M4_WAVES",    "AWQ_M4_RPW",
-    "AWQ_DECODE_MFMA", "AWQ_DECODE_M4",  "AWQ_SMALLM_MFMA",  "AWQ_SKINNY",      "AWQ_SKINNY_SPLITS"};
+    "AWQ_DECODE_MFMA", "AWQ_DECODE_M4",  "AWQ_SMALLM_MFMA",  "AWQ_SKINNY",      "AWQ_SKINNY_SPLITS",
+    "AWQ_SKINNY_COLS"};
 static std::atomic<int> g_tune_val[kTuneCount];
 static std::atomic<bool> g_tune_set[kTuneCount];
 static std::once_flag g_tune_once;
@@ -328,16 +329,19 @@ void* workspace_get(hipStream_t stream, size_t bytes, int slot) {
 
 // ---------------------------------------------------------------------------
 // Static split-K scratch of awq_gemm_noalloc: a file-scope device array,
-// one copy per GPU, held for the life of the process. The first 1 MiB holds
-// arrival counters (zero between calls: every split-K kernel re-arms the
-// counters it uses), the rest fp32 partial sums. Host code never names the
+// one copy per GPU, held for the life of the process: 1 MiB of arrival
+// counters (zero between calls: every split-K kernel re-arms the counters it
+// uses), 63 MiB of fp32 partial sums, and 64 MiB for fp32 activations split
+// into f16 hi + lo rows (the fp32 prefill's prepass). Host code never names the
 // array itself (its host-side name is not a device address): its address on
 // each device comes from hipGetSymbolAddress, looked up once per device on
 // the first awq_gemm_noalloc call there, which also clears the counters with
 // a fill kernel on the caller's stream.
 // ---------------------------------------------------------------------------
 constexpr size_t kScratchCounterBytes = size_t(1) << 20;
-constexpr size_t kScratchBytes = size_t(64) << 20;
+constexpr size_t kScratchPartialBytes = (size_t(63) << 20);
+constexpr size_t kScratchXSplitBytes = size_t(64) << 20;
+constexpr size_t kScratchBytes = kScratchCounterBytes + kScratchPartialBytes + kScratchXSplitBytes;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 __global__ void fill_zero_u32(uint32_t* p, uint32_t n) {
@@ -365,15 +369,19 @@ static void* scratch_on_device(hipStream_t stream) {
 
 void* ws_get(const GemmProblem& p, size_t bytes, int slot) {
   if (!p.scratch) return workspace_get(p.stream, bytes, slot);
-  const size_t cap = slot == kWsCounters ? kScratchCounterBytes : kScratchBytes - kScratchCounterBytes;
+  const size_t cap = slot == kWsCounters ? kScratchCounterBytes
+                   : slot == kWsPartials ? kScratchPartialBytes : kScratchXSplitBytes;
+  const size_t off = slot == kWsCounters ? 0
+                   : slot == kWsPartials ? kScratchCounterBytes : kScratchCounterBytes + kScratchPartialBytes;
   if (bytes > cap) {
     std::ostringstream os;
-    os << "awq_gemm_noalloc: this call needs " << bytes << " bytes of split-K "
-       << (slot == kWsCounters ? "counters" : "partial sums") << ", more than the " << cap
-       << " bytes of the static scratch (awq_gemm has no such limit)";
+    os << "awq_gemm_noalloc: this call needs " << bytes << " bytes of "
+       << (slot == kWsCounters ? "split-K counters" : slot == kWsPartials ? "split-K partial sums"
+                                                                          : "split fp32 activations")
+       << ", more than the " << cap << " bytes of the static scratch (awq_gemm has no such limit)";
     panic(os.str());
   }
-  return static_cast<char*>(p.scratch) + (slot == kWsCounters ? 0 : kScratchCounterBytes);
+  return static_cast<char*>(p.scratch) + off;
 }
 
 static int64_t numel(const awq_tensor_ref& t) {

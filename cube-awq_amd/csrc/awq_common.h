@@ -173,6 +173,7 @@ struct GemmProblem {
   int32_t act;    // 1: gate/up interleaved by column, y [rows, N/2] = SiLU(gate) * up
   hipStream_t stream;
   void* scratch;  // static split-K scratch (awq_gemm_noalloc), or null: library workspace
+  const float* xrowfac;  // fp32 activations split into f16 hi + lo: row factors (else null)
 };
 
 struct DequantProblem {
@@ -222,6 +223,7 @@ enum TuneKey {
   kTuneSmallMMfma,    // AWQ_SMALLM_MFMA
   kTuneSkinny,        // AWQ_SKINNY
   kTuneSkinnySplits,  // AWQ_SKINNY_SPLITS
+  kTuneSkinnyCols,    // AWQ_SKINNY_COLS
   kTuneCount
 };
 // The override's value (atoi of the variable), or dflt when it is unset.
@@ -238,7 +240,9 @@ void ensure_dyn_smem(const void* kernel, int bytes, const char* what);
 // never freed once handed out (a graph captured on the stream may still
 // hold it), so growth allocates a new one and retires the old one for the
 // life of the process. Growth is refused during stream capture.
-enum { kWsCounters = 0, kWsPartials = 1 };
+// kWsXSplit holds fp32 activations split into f16 hi and lo rows and their
+// row factors (M K 4 + M 4 bytes), written by a prepass of the same call.
+enum { kWsCounters = 0, kWsPartials = 1, kWsXSplit = 2 };
 void* workspace_get(hipStream_t stream, size_t bytes, int slot);
 // The split-K buffer of one launch of problem p: a region of p.scratch when
 // it is set (awq_gemm_noalloc; sizes past the region are an error, nothing is

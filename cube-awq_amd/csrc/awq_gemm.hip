@@ -52,7 +52,15 @@ namespace {
 
 constexpr int kBK = 64;
 
-enum { MODE_F16 = 0, MODE_BF16 = 1, MODE_F32 = 2 };
+// MODE_F32S: fp32 activations on the f16 matrix cores. A prepass
+// (x_split_kernel) writes each row of x, scaled by the power of two 2^e that
+// puts its largest |x| in [2^14, 2^15), as f16 hi + lo (hi = f16(x 2^e),
+// lo = f16(x 2^e - hi)) and the row factor 2^-e. The large-tile kernel
+// multiplies both halves with the exact f16 integers q - z (no rounding of
+// the weight at all), sums each quantisation group in fp32, applies the
+// group's scale s to that sum in fp32, and the row factor at the end: fp32
+// accuracy at about half the f16 rate.
+enum { MODE_F16 = 0, MODE_BF16 = 1, MODE_F32 = 2, MODE_F32S = 3 };
 
 template <int MODE> struct ModeT;
 template <> struct ModeT<MODE_F16> {
@@ -66,6 +74,9 @@ template <> struct ModeT<MODE_BF16> {
 template <> struct ModeT<MODE_F32> {
   typedef float T;
   static constexpr int kPad = 4;
+};
+template <> struct ModeT<MODE_F32S> {
+  typedef f16_t T;
 };
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -94,6 +105,10 @@ struct GemmArgs {
   int32_t splits, stages_per_split;
   float* partial;
   uint32_t* counters;
+  // MODE_F32S: x is the prepass output, hi [M][K] f16 then lo [M][K] f16
+  // (lo_off = M K 2 bytes after hi), and rowfac [M] the row factors 2^-e.
+  const float* rowfac;
+  uint32_t lo_off;
 };
 
 constexpr int kTileCtrStride = 64;  // u32 words between per-tile counters (256 B)
@@ -437,14 +452,15 @@ struct BigTile {
   static constexpr int kPacks = BN / 8;                         // packed words per W row
   static constexpr int kRW = (64 * kPacks / kThreads >= 8) ? 8 : 4;  // W rows per thread
   static constexpr int kWThreads = kPacks * (kBK / kRW);
-  static constexpr int kABytes = BM * kRowBytes;  // one X buffer
+  static constexpr int kXParts = MODE == MODE_F32S ? 2 : 1;  // hi and lo rows
+  static constexpr int kABytes = BM * kRowBytes * kXParts;  // one X buffer
   static constexpr int kBBytes = BN * kRowBytes;  // one W buffer
   // X is prefetched two stages ahead: three X buffers when they fit in the
   // 160 KB of LDS next to the two W buffers.
   static constexpr int kNA = (3 * kABytes + 2 * kBBytes <= 160 * 1024) ? 3 : 2;
   // Layout: X buffers 0..kNA-1, then W buffers 0, 1.
   static constexpr size_t kSmem = (size_t)kNA * kABytes + 2 * (size_t)kBBytes;
-  static_assert(MODE != MODE_F32, "large-tile kernel is f16/bf16 only");
+  static_assert(MODE != MODE_F32, "large-tile kernel is f16/bf16 (or fp32 split into f16 hi + lo)");
   static_assert(kWThreads <= kThreads, "W tile needs more threads");
   static_assert((BM / 8) % (kThreads / 64) == 0, "X tile must split evenly over the waves");
   static_assert(MS == 32 || MS == 16, "MFMA shape");
@@ -455,6 +471,8 @@ template <int MODE, int ST, int BM, int BN, int WGM, int WGN, int MS, bool SEQ, 
 __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a) {
   using C = BigTile<MODE, BM, BN, WGM, WGN, MS>;
   using S = typename Elem<ST>::type;
+  constexpr bool F32S = MODE == MODE_F32S;
+  static_assert(!F32S || (!PP && MS == 32), "fp32 split mode runs the single-phase 32x32 schedule");
   constexpr int RW = C::kRW;
   constexpr int kSW = (sizeof(S) * 8) / 4;  // dwords holding a pack's 8 scales
   extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -498,7 +516,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     if constexpr (PP) return (wave / (NW / 2)) * (BM / 16) + wave % (NW / 2) + i * (NW / 2);
     else return wave + i * NW;
   };
-  const rsrc_t xres = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
+  const rsrc_t xres = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2 * C::kXParts));
   uint32_t xvoff[kXIns];
 #pragma unroll
   for (int i = 0; i < kXIns; ++i) {
@@ -529,10 +547,14 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 
   // Two register sets for packed W / zeros / scales, used alternately: one
   // being dequantised, the other in flight two stages ahead.
+  // F32S: cs holds this lane's output-column scales (one per block column
+  // j) of the stage's group, applied to the group's sums.
+  constexpr int kCS = F32S ? C::kJ : 0;
   struct WRegs {
     uint32_t w[RW];
     uint32_t z;
     uint32_t sv[kSW];
+    float cs[kCS > 0 ? kCS : 1];
   };
   // W(j) lives in wr[j % 2]: loaded two stages ahead of its MFMAs.
   WRegs wr[2];
@@ -552,6 +574,21 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       const u32x4 q = __builtin_amdgcn_raw_buffer_load_b128(sres, soff + v * 4, 0, 0);
       r_.sv[v] = q[0]; r_.sv[v + 1] = q[1]; r_.sv[v + 2] = q[2]; r_.sv[v + 3] = q[3];
     }
+    if constexpr (F32S) {
+      // One VMEM load per block column, issued with the stage's other loads
+      // (the explicit vmcnt counts below include them).
+#pragma unroll
+      for (int j = 0; j < kCS; ++j) {
+        const int col = min(n0 + wn * C::kWTN + 32 * j + (lane & 31), a.N - 1);
+        const uint32_t o = (uint32_t)(grp * a.N + col) * (uint32_t)sizeof(S);
+        if constexpr (sizeof(S) == 4) {
+          r_.cs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sres, o, 0, 0));
+        } else {
+          const uint16_t hbits = __builtin_amdgcn_raw_buffer_load_b16(sres, o, 0, 0);
+          r_.cs[j] = to_f32(__builtin_bit_cast(S, hbits));
+        }
+      }
+    }
   };
   auto scale_of = [&](const uint32_t (&sv)[kSW], int c) -> float {
     if constexpr (sizeof(S) == 4) return __builtin_bit_cast(float, sv[c]);
@@ -567,6 +604,12 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     for (int i = 0; i < kXIns; ++i) {
       lds_dma16(xres, smem_raw + buf * C::kABytes + xchunk(i) * 1024, xvoff[i], koff);
     }
+    if constexpr (F32S) {  // the lo rows, BM rows after the hi rows in LDS
+#pragma unroll
+      for (int i = 0; i < kXIns; ++i)
+        lds_dma16(xres, smem_raw + buf * C::kABytes + BM * C::kRowBytes + xchunk(i) * 1024, xvoff[i],
+                  koff + a.lo_off);
+    }
   };
 
   // Dequantise column c of the pack (RW k values) and write it to W buffer
@@ -575,7 +618,16 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     uint32_t dq[RW / 2];
     const int L = lane_of_col<SEQ>(c);
     const uint32_t zw = r_.z;
-    if constexpr (MODE == MODE_F16) {
+    if constexpr (F32S) {
+      // Exact f16 integers q - z: magic numbers of the nibble and the zero,
+      // one exact v_pk_add_f16; the scale is applied to the group's sums.
+      const f16x2 fz = __builtin_bit_cast(f16x2, nib_f16x2(zw, zw, L));
+#pragma unroll
+      for (int r = 0; r < RW / 2; ++r) {
+        const f16x2 fv = __builtin_bit_cast(f16x2, nib_f16x2(r_.w[2 * r], r_.w[2 * r + 1], L));
+        dq[r] = __builtin_bit_cast(uint32_t, fv - fz);
+      }
+    } else if constexpr (MODE == MODE_F16) {
       // Nibbles of packed lane L as f16 magic numbers (1024 + q or 64 + q),
       // zero likewise; (v - zc) is exact and * sc rounds once.
       const uint32_t zc = nib_f16x2(zw, zw, L);
@@ -634,10 +686,19 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // ---- MFMA operand addressing -------------------------------------------
   typedef float AccT __attribute__((ext_vector_type(MS == 32 ? 16 : 4)));
   AccT acc[C::kI][C::kJ];
+  // F32S: the current group's sums (MFMA target), folded into acc with the
+  // group's column scales gsc at the group's end.
+  constexpr int kPI = F32S ? C::kI : 1, kPJ = F32S ? C::kJ : 1;
+  AccT pacc[kPI][kPJ];
+  float gsc[kPJ];
 #pragma unroll
   for (int i = 0; i < C::kI; ++i)
 #pragma unroll
     for (int j = 0; j < C::kJ; ++j) acc[i][j] = AccT{};
+#pragma unroll
+  for (int i = 0; i < kPI; ++i)
+#pragma unroll
+    for (int j = 0; j < kPJ; ++j) pacc[i][j] = AccT{};
   // 16x16x32: lane l reads row (l & 15) of a block, granule 4 kq + (l >> 4);
   // the slice kq flips granule bit 2 (kq << 6 in bytes), so one base per
   // block row plus an XOR.
@@ -668,8 +729,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   const uint32_t b_fl = (uint32_t)(((wn * (C::kWTN / 8)) & 4) << 4);
   const uint32_t a_par[2] = {a_base ^ a_fl, a_base ^ a_fl ^ 64u};
   const uint32_t b_par[2] = {b_base ^ b_fl, b_base ^ b_fl ^ 64u};
-  typedef typename std::conditional<MODE == MODE_F16, f16x8, bf16x8>::type V8;
-  typedef V8 Frags[C::kI + C::kJ];
+  typedef typename std::conditional<MODE == MODE_BF16, bf16x8, f16x8>::type V8;
+  // X fragments (kI), W fragments (kJ), and for F32S the lo X fragments (kI).
+  constexpr int kFA2 = F32S ? C::kI : 0;
+  typedef V8 Frags[C::kI + C::kJ + kFA2];
   auto read_frags = [&](int abuf, int bbuf, int kq, Frags& f) {
     if constexpr (MS == 16) {
 #pragma unroll
@@ -688,8 +751,27 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     for (int j = 0; j < C::kJ; ++j)
       f[C::kI + j] = *reinterpret_cast<const V8*>(smem_raw + (b_par[j & 1] ^ (uint32_t)(kq << 5)) +
                                                   (bbuf * C::kBBytes + j * 32 * C::kRowBytes));
+    if constexpr (F32S) {
+      // lo rows: BM rows further; (BM + r) has the swizzle of r (BM % 64 == 0).
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i)
+        f[C::kI + C::kJ + i] = *reinterpret_cast<const V8*>(
+            smem_raw + (a_par[i & 1] ^ (uint32_t)(kq << 5)) +
+            (abuf * C::kABytes + (BM + i * 32) * C::kRowBytes));
+    }
   };
   auto mfmas = [&](const Frags& f) {
+    if constexpr (F32S) {
+#pragma unroll
+      for (int i = 0; i < C::kI; ++i)
+#pragma unroll
+        for (int j = 0; j < C::kJ; ++j) {
+          pacc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[i], f[C::kI + j], pacc[i][j], 0, 0, 0);
+          pacc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f[C::kI + C::kJ + i], f[C::kI + j], pacc[i][j],
+                                                               0, 0, 0);
+        }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < C::kI; ++i)
 #pragma unroll
@@ -719,7 +801,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 
   // VMEM instructions one stage issues: packed W rows, the zero word, the
   // scales (16 bytes each), the LDS-direct X granules.
-  constexpr int kVmPerStage = RW + 1 + (kSW + 3) / 4 + kXIns;
+  constexpr int kVmPerStage = RW + 1 + (kSW + 3) / 4 + kCS + kXIns * C::kXParts;
   static_assert(kVmPerStage < 64, "vmcnt range");
   constexpr int kNA = C::kNA;
   // End-of-stage wait: with three X buffers the X loads of stage s+1 were
@@ -831,6 +913,10 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
 #pragma unroll
   for (int c = 0; c < 8; ++c) deq_store_col(wr[0], c, 0);
+  if constexpr (F32S) {
+#pragma unroll
+    for (int j = 0; j < kPJ; ++j) gsc[j] = wr[0].cs[j];
+  }
   load_w(min(1, stages - 1), wr[1]);
   if constexpr (kNA == 3) load_x(min(1, stages - 1), 1);
   __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmWait, 0));
@@ -849,9 +935,9 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   // tail the prefetches clamp to the last stage and land in buffers nobody
   // reads any more.
   auto interleave = [&]() {
-    constexpr int kM = C::kI * C::kJ;
-    constexpr int kValu = MS == 32 ? 4 : 3;  // VALU ops after each MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, C::kI + C::kJ, 0);  // DS read
+    constexpr int kM = C::kI * C::kJ * (F32S ? 2 : 1);
+    constexpr int kValu = F32S ? 2 : MS == 32 ? 4 : 3;  // VALU ops after each MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, C::kI + C::kJ + kFA2, 0);  // DS read
 #pragma unroll
     for (int q = 0; q < kM; ++q) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -883,6 +969,24 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       interleave();
     }
     __builtin_amdgcn_sched_barrier(0);
+    if constexpr (F32S) {
+      // End of the group (or of this workgroup's K run): fold the group's
+      // sums into acc with its column scales. Then take the scales of stage
+      // s+1 (its W registers have landed: they were just dequantised).
+      const int gs = s_begin + s;
+      if (((gs + 1) & ((1 << a.grp_shift) - 1)) == 0 || s + 1 == stages) {
+#pragma unroll
+        for (int i = 0; i < C::kI; ++i)
+#pragma unroll
+          for (int j = 0; j < C::kJ; ++j) {
+#pragma unroll
+            for (int r = 0; r < kAccN; ++r) acc[i][j][r] = __builtin_fmaf(gsc[j], pacc[i][j][r], acc[i][j][r]);
+            pacc[i][j] = AccT{};
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < kPJ; ++j) gsc[j] = deq.cs[j];
+    }
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(kVmWait, 0));
     __builtin_amdgcn_s_barrier();
   };
@@ -899,6 +1003,17 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 
   // ---- epilogue --------------------------------------------------------------
+  if constexpr (F32S) {
+    // Undo the row scaling 2^e of the prepass (exact: a power of two).
+#pragma unroll
+    for (int i = 0; i < C::kI; ++i)
+#pragma unroll
+      for (int r = 0; r < kAccN; ++r) {
+        const float rf = a.rowfac[min(out_row(i, r), a.M - 1)];
+#pragma unroll
+        for (int j = 0; j < C::kJ; ++j) acc[i][j][r] *= rf;
+      }
+  }
   if (a.splits > 1) {
     // Split-K: publish this split's tile with agent-scope (write-through)
     // stores, wait for them, count the arrival; the last workgroup of the tile
@@ -1018,6 +1133,53 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
   }
 }
 
+// Prepass of MODE_F32S: one workgroup per row of x [M, K] f32 (K % 4 == 0).
+// The row's largest finite |x| gives e with max |x| 2^e in [2^14, 2^15)
+// (e = 0 for a row of zeros or with no finite value, clamped to +-126 so
+// 2^-e stays a normal float); then hi = f16(x 2^e), lo = f16(x 2^e - hi)
+// (x 2^e is exact, and so is x 2^e - hi: both lie in one binade of f32), so
+// |x - (hi + lo) 2^-e| <= 2^-22 max |x|. Outputs: hi [M][K], lo [M][K]
+// (f16), rowfac [M] = 2^-e. Non-finite values stay non-finite.
+__global__ __launch_bounds__(256) void x_split_kernel(const float* __restrict__ x, f16_t* __restrict__ hi,
+                                                      f16_t* __restrict__ lo, float* __restrict__ rowfac,
+                                                      int K) {
+  __shared__ float wmax[4];
+  const int64_t row = (int64_t)blockIdx.x * K;
+  const float4* xr = reinterpret_cast<const float4*>(x + row);
+  const int n4 = K >> 2;
+  float mx = 0.f;
+  for (int i = threadIdx.x; i < n4; i += 256) {
+    const float4 v = xr[i];
+    const float m4 = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    mx = (m4 <= 3.4028234e38f) ? fmaxf(mx, m4) : mx;  // finite values only (NaN, inf skipped)
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+  int e = 0;
+  if (mx > 0.f) {
+    int E;
+    frexpf(mx, &E);  // mx in [2^(E-1), 2^E)
+    e = min(max(15 - E, -126), 126);
+  }
+  if (threadIdx.x == 0) rowfac[blockIdx.x] = ldexpf(1.f, -e);
+  typedef f16_t h4_t __attribute__((ext_vector_type(4)));
+  for (int i = threadIdx.x; i < n4; i += 256) {
+    const float4 v = xr[i];
+    const float t[4] = {ldexpf(v.x, e), ldexpf(v.y, e), ldexpf(v.z, e), ldexpf(v.w, e)};
+    h4_t h, l;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      h[q] = (f16_t)t[q];
+      l[q] = (f16_t)(t[q] - (float)h[q]);
+    }
+    *reinterpret_cast<h4_t*>(hi + row + 4 * i) = h;
+    *reinterpret_cast<h4_t*>(lo + row + 4 * i) = l;
+  }
+}
+
 // Row tiles per raster group. An XCD runs about CUs/8 tiles at once; with a
 // rows by b columns of them (a*b fixed) it fetches a*BM + b*BN/4 row-bytes of
 // X and W per K step (f16 X, 4-bit W), least near a = sqrt(CUs/8 * BN / (4 BM)).
@@ -1053,6 +1215,8 @@ void launch_big_act(const GemmProblem& p, int splits) {
   a.swizzled_tiles = tiles & ~7;
   a.group_m = raster_group_m(a.tiles_m, BM, BN);
   a.grp_shift = __builtin_ctzll(p.group / kBK);
+  a.rowfac = p.xrowfac;
+  a.lo_off = (uint32_t)(p.rows * p.K * 2);
   const int total_stages = (int)(p.K / kBK);
   // Partials are addressed through a 32-bit buffer range.
   while (splits > 1 && (int64_t)splits * p.rows * p.N * 4 >= (1ll << 32)) --splits;
@@ -1215,7 +1379,14 @@ void launch_mode(const GemmProblem& p) {
     }
   }
   if (int v = tuning(kTuneGemmSplits, 0); v >= 1) splits = v;
-  if constexpr (MODE != MODE_F32) {
+  if constexpr (MODE == MODE_F32S) {
+    // X tiles hold hi and lo rows, so 256-row tiles do not fit the LDS: the
+    // 128 x 256 tile (8 waves) where a 256-row or wide tile was chosen,
+    // else 128 x 128 (4 waves), with the split count chosen above.
+    if (cfg == 3 || cfg == 2 || cfg == 6 || cfg == 7 || cfg == 8 || cfg == 9 || cfg == 10)
+      return launch_big<MODE, ST, 128, 256, 2, 4, 32, SEQ>(p, splits);
+    return launch_big<MODE, ST, 128, 128, 2, 2, 32, SEQ>(p, splits);
+  } else if constexpr (MODE != MODE_F32) {
     switch (cfg) {
       case 2: return launch_big<MODE, ST, 256, 256, 2, 4, 32, SEQ>(p, splits);
       case 3: return launch_big<MODE, ST, 128, 256, 2, 4, 32, SEQ>(p, splits);
@@ -1228,7 +1399,7 @@ void launch_mode(const GemmProblem& p) {
       default: break;
     }
   }
-  launch_cfg<MODE, ST, 128, 128, 2, 2, SEQ>(p);
+  if constexpr (MODE != MODE_F32S) launch_cfg<MODE, ST, 128, 128, 2, 2, SEQ>(p);
 }
 
 template <int MODE>
@@ -1277,6 +1448,37 @@ void launch_gemm(const GemmProblem& p) {
     const double slice = 12.0 + (double)p.K * (double)p.N / 2.0 / 2.4e6;
     return (double)((p.rows + 15) / 16) * slice < generic;
   };
+  // fp32 activations on the f16 matrix cores (MODE_F32S), where the
+  // large-tile kernel takes the shape, from 33 rows: at 17..32 two 16-row
+  // slices are faster (4096 -> 14336: 32 against 74 us at M = 17; 79 us
+  // against 95 for four slices at M = 64, 522 us at M = 2048 against
+  // ~2.4 ms on the fp32-MFMA kernel). AWQ_F32_SLICES=2 forces slices.
+  const int64_t gsz = p.group / kBK;
+  const bool f32s_ok = p.xt == AWQ_F32 && p.rows > 32 && p.K % kBK == 0 && p.group % kBK == 0 &&
+                       (gsz & (gsz - 1)) == 0 && p.rows * p.K * 4 < (1ll << 32) &&
+                       p.K * (p.N / 8) * 4 < (1ll << 32) && (p.K / p.group) * p.N * 4 < (1ll << 32) &&
+                       f32_slices != 2 && tuning(kTuneGemmTile, 0) != 1;
+  if (f32s_ok) {
+    const size_t split_bytes = (size_t)p.rows * p.K * 4;
+    char* xs = static_cast<char*>(ws_get(p, split_bytes + (size_t)p.rows * 4, kWsXSplit));
+    GemmProblem q = p;
+    q.x = xs;
+    q.xrowfac = reinterpret_cast<const float*>(xs + split_bytes);
+    hipLaunchKernelGGL(x_split_kernel, dim3((unsigned)p.rows), dim3(256), 0, p.stream,
+                       static_cast<const float*>(p.x), reinterpret_cast<f16_t*>(xs),
+                       reinterpret_cast<f16_t*>(xs + split_bytes / 2), reinterpret_cast<float*>(xs + split_bytes),
+                       (int)p.K);
+    check_hip(hipGetLastError(), "x split kernel launch");
+    if (p.order == AWQ_ORDER_SEQUENTIAL) {
+      AWQ_ASSERT(p.st == AWQ_F32, "sequential-order GEMM needs scales in the input dtype");
+      return launch_mode<MODE_F32S, AWQ_F32, true>(q);
+    }
+    switch (p.st) {
+      case AWQ_F32: return launch_mode<MODE_F32S, AWQ_F32, false>(q);
+      case AWQ_F16: return launch_mode<MODE_F32S, AWQ_F16, false>(q);
+      default: return launch_mode<MODE_F32S, AWQ_BF16, false>(q);
+    }
+  }
   if (p.xt == AWQ_F32 && p.rows > 16 && p.group % 32 == 0 && p.K % 32 == 0 && f32_slices != 0 &&
       slices_win()) {
     const int64_t y_row = (p.act ? p.N / 2 : p.N) * dtype_size(p.yt);

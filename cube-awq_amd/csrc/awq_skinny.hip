@@ -11,17 +11,22 @@
 // barrier, MFMA round trip, and on wide outputs its tiles already fill the
 // CUs, so K splits cannot hide that. Here the weights stream as in the decode
 // kernels:
-//  * A workgroup owns 256 columns (32 packed words = 128 bytes of each row)
-//    and a run of K; 32-row steps of W, the matching 32 columns of X and,
+//  * A workgroup owns a chunk of 256 columns (32 packed words = 128 bytes of
+//    each row; 8 waves of 32 columns) or, on outputs narrower than 6144
+//    columns, 64 (8 packed words; 4 waves of 16 columns, one MFMA tile each,
+//    chunks placed so each XCD runs a contiguous run of them and their
+//    32-byte row pieces share 128-byte lines in its L2), and a run of K;
+//    32-row steps of W, the matching 32 columns of X and,
 //    up front, the zeros and scales of the run's groups go global -> LDS
 //    directly (buffer_load ... lds, 16 bytes per lane for W and X, 4 for the
 //    zeros and scales) into a ring of kRing steps, kRing - 2 steps ahead,
 //    with explicit vmcnt waits and one s_barrier per two steps.
-//  * 8 waves: wave w takes packs 4 w .. 4 w + 3 (32 columns, two 16-column
-//    MFMA tiles) for every 16-row tile, so each weight is dequantised once.
-//    Lane (lg = lane / 16, lj = lane % 16) reads the 8 words of rows
-//    8 lg .. 8 lg + 7 of pack 4 w + (lj & 3) from LDS and builds the B operand
-//    of tile t from packed lane c = 4 t + (lj >> 2): one v_perm_b32 gathers
+//  * 256 columns: wave w takes packs 4 w .. 4 w + 3 (32 columns, two
+//    16-column MFMA tiles) for every 16-row tile, so each weight is
+//    dequantised once. Lane (lg = lane / 16, lj = lane % 16) reads the 8
+//    words of rows 8 lg .. 8 lg + 7 of pack 4 w + (lj & 3) from LDS and
+//    builds the B operand of tile t from packed lane c = 4 t + (lj >> 2)
+//    (64 columns: pack 2 w + (lj & 1), packed lane lj >> 1): one v_perm_b32 gathers
 //    byte c / 2 of two rows, one v_bitop3_b32 makes the f16 magic 1024 + q
 //    (64 + q for the high nibble), then an exact v_pk_add_f16 of -(1024 + z)
 //    and one v_pk_mul_f16 by s: 2 VALU ops per weight. bf16 (no packed bf16
@@ -51,14 +56,30 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kCols = 256;          // columns per workgroup (chunk)
-constexpr int kPacks = kCols / 8;   // packed words per row of a chunk
 constexpr int kStep = 32;           // K rows per step (one MFMA k-block)
 constexpr int kRing = 8;            // steps held in LDS
-constexpr int kWBlock = 8 * 128 + 32;  // eight 128-byte W rows + pad (bank spread)
-constexpr int kWSlot = (kStep / 8) * kWBlock;
-constexpr int kMaxGroups = 36;      // groups a workgroup's K run may touch
 constexpr int kCtrStride = 64;      // u32 words between arrival counters
+
+// Layout constants of a chunk width CW (columns per workgroup): 256 (8 waves
+// of 32 columns, two 16-column MFMA tiles each) or 64 (4 waves of 16 columns,
+// one tile each).
+template <int CW>
+struct Chunk {
+  static constexpr int kWaves = CW == 256 ? 8 : 4;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kPacks = CW / 8;               // packed words per row
+  static constexpr int kPPW = kPacks / kWaves;         // packs per wave (4 or 2)
+  static constexpr int kT = kPPW / 2;                  // 16-column MFMA tiles per wave
+  static constexpr int kRowBytes = CW / 2;             // one packed W row
+  // W: wave i < 4 moves rows 8 i .. 8 i + 7 of a step (one DMA: 16 bytes per
+  // lane for 128-byte rows, 4 for 32-byte rows) into a padded 8-row block
+  // (the pad spreads the blocks over the LDS banks).
+  static constexpr int kWBlock = 8 * kRowBytes + (CW == 256 ? 32 : 16);
+  static constexpr int kWSlot = (kStep / 8) * kWBlock;
+  static constexpr int kMaxGroups = CW == 256 ? 36 : 128;  // groups a K run may touch
+  static constexpr int kXWave0 = kWaves - 4;           // first wave loading X
+  static_assert(kT >= 1 && kPPW * kWaves == kPacks, "chunk layout");
+};
 
 struct SkinnyArgs {
   const void* x;
@@ -73,6 +94,8 @@ struct SkinnyArgs {
   int32_t M, K, N, group;
   int32_t splits, steps_per_split;
   int32_t seq;         // sequential nibble order
+  int32_t chunks;      // column chunks (grid.x)
+  int32_t xcd_chunks;  // leading chunks covered by the XCD mapping (multiple of 8)
 };
 
 constexpr int waitcnt_vm(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -93,27 +116,32 @@ __device__ __forceinline__ int xswz(int r) { return (r >> 2) & 3; }
 // ACT: the gate/up SiLU epilogue (store_out; AutoAWQ order only), a template
 // parameter so the plain kernel's code is untouched by it. BF: bf16
 // activations (16-bit scales), W dequantised through f32 (see compute).
-template <int MT, bool ACT, bool BF>
-__global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
+template <int MT, bool ACT, bool BF, int CW>
+__global__ __launch_bounds__(Chunk<CW>::kThreads) void skinny_kernel(SkinnyArgs a) {
+  using C = Chunk<CW>;
   typedef typename std::conditional<BF, bf16x8_t, f16x8_t>::type XV;
-  constexpr int kT = 2;                        // 16-column MFMA tiles per wave
+  constexpr int kT = C::kT;
+  constexpr int kPacks = C::kPacks;
   constexpr int kXRows = 16 * MT;
   constexpr int kXSlot = kXRows * 64;          // 32 f16 columns of X per row
-  // 16-byte DMAs per step: W rows 8 i .. 8 i + 7 by wave i (i < 4); X rows
-  // 16 j .. 16 j + 15 by wave 4 + j % 4 (MT of them).
+  // 16-byte DMAs per step for X: rows 16 j .. 16 j + 15 by X wave j % 4.
   constexpr int kXPerWave = (MT + 3) / 4;
   static_assert(MT >= 2 && MT <= 8, "row tiles");
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* wring = smem;                               // kRing W slots
-  unsigned char* xring = smem + kRing * kWSlot;              // kRing X slots
-  uint32_t* zlds = reinterpret_cast<uint32_t*>(xring + kRing * kXSlot);  // [groups][32] zero words
-  unsigned char* slds = reinterpret_cast<unsigned char*>(zlds + kMaxGroups * kPacks);  // [groups][256] scales
+  unsigned char* xring = smem + kRing * C::kWSlot;           // kRing X slots
+  uint32_t* zlds = reinterpret_cast<uint32_t*>(xring + kRing * kXSlot);  // [groups][kPacks] zero words
+  unsigned char* slds = reinterpret_cast<unsigned char*>(zlds + C::kMaxGroups * kPacks);  // [groups][CW] scales
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lg = lane >> 4, lj = lane & 15;
-  const int chunk = blockIdx.x, split = blockIdx.y;
+  // Consecutive workgroups go to different XCDs: remap so each XCD runs a
+  // contiguous run of chunks, whose rows share 128-byte lines in its L2.
+  int chunk = blockIdx.x;
+  if (chunk < a.xcd_chunks) chunk = (chunk & 7) * (a.xcd_chunks >> 3) + (chunk >> 3);
+  const int split = blockIdx.y;
   const int np = a.N >> 3;
   const int s0 = split * a.steps_per_split;
   const int steps = min(a.steps_per_split, a.K / kStep - s0);
@@ -122,26 +150,42 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   const int es = a.st == AWQ_F32 ? 4 : 2;
 
   // ---- prologue DMAs: zeros and scales of the run's groups (wave 0 and 1),
-  // then the first kRing - 1 steps of W and X (every wave) ---------------------
+  // then the first kRing - 2 steps of W and X (every wave) ---------------------
   const int ngroups = (k_begin + steps * kStep - 1) / a.group - g_first + 1;
-  const rsrc_t zres = make_rsrc(a.qzeros, (uint32_t)((a.K / a.group) * np * 4));
-  const rsrc_t sres = make_rsrc(a.scales, (uint32_t)((int64_t)(a.K / a.group) * a.N * es));
+  const int ngroups_all = a.K / a.group;
+  const rsrc_t zres = make_rsrc(a.qzeros, (uint32_t)(ngroups_all * np * 4));
+  const rsrc_t sres = make_rsrc(a.scales, (uint32_t)((int64_t)ngroups_all * a.N * es));
   if (wave == 0) {
-    // lane l: zero word of pack (l & 31) of group 2 i + (l >> 5)
-    for (int gi = 0; gi < ngroups; gi += 2) {
-      const int gr = gi + (lane >> 5);
-      const int pk = min(chunk * kPacks + (lane & 31), np - 1);
-      const int grc = min(g_first + gr, a.K / a.group - 1);
+    // lane l: zero word of pack l % kPacks of group gi + l / kPacks
+    constexpr int kGpi = 64 / kPacks;  // groups per instruction
+    for (int gi = 0; gi < ngroups; gi += kGpi) {
+      const int pk = min(chunk * kPacks + (lane % kPacks), np - 1);
+      const int grc = min(g_first + gi + lane / kPacks, ngroups_all - 1);
       dma4(zres, reinterpret_cast<unsigned char*>(zlds + gi * kPacks), (uint32_t)(grc * np + pk) * 4u, 0);
     }
   } else if (wave == 1) {
-    // scales of the chunk's 256 columns per group: 512 (f16) or 1024 (f32) bytes
-    const int row_bytes = kCols * es;
-    for (int gi = 0; gi < ngroups; ++gi) {
-      const int grc = min(g_first + gi, a.K / a.group - 1);
-      for (int o = 0; o < row_bytes; o += 256) {
-        const int col_byte = min(chunk * kCols * es + o + lane * 4, a.N * es - 4);
-        dma4(sres, slds + gi * kCols * 4 + o, (uint32_t)((int64_t)grc * a.N * es + col_byte), 0);
+    // scales of the chunk's CW columns per group, CW * es bytes, stored at a
+    // CW * 4-byte pitch
+    const int row_bytes = CW * es;
+    if (row_bytes >= 256) {
+      for (int gi = 0; gi < ngroups; ++gi) {
+        const int grc = min(g_first + gi, ngroups_all - 1);
+        for (int o = 0; o < row_bytes; o += 256) {
+          const int col_byte = min(chunk * CW * es + o + lane * 4, a.N * es - 4);
+          dma4(sres, slds + gi * CW * 4 + o, (uint32_t)((int64_t)grc * a.N * es + col_byte), 0);
+        }
+      }
+    } else {
+      // one instruction covers 256 / row_bytes groups: lane l -> group
+      // gi + l / (row_bytes / 4), byte 4 (l % (row_bytes / 4)); each group's
+      // row lands at its CW * 4 pitch only if 256 / row_bytes == 1, so the
+      // lanes of later groups go through separate instructions.
+      const int lpg = row_bytes / 4;  // lanes per group row
+      for (int gi = 0; gi < ngroups; ++gi) {
+        const int grc = min(g_first + gi, ngroups_all - 1);
+        const int col_byte = min(chunk * CW * es + (lane % lpg) * 4, a.N * es - 4);
+        if (lane < lpg)
+          dma4(sres, slds + gi * CW * 4, (uint32_t)((int64_t)grc * a.N * es + col_byte), 0);
       }
     }
   }
@@ -149,13 +193,15 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   const rsrc_t wres = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
   const rsrc_t xres = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
   const uint32_t row_bytes_w = (uint32_t)np * 4u;
-  // W (waves 0..3): wave i moves rows 8 i .. 8 i + 7 of a step; lane l -> row
-  // 8 i + (l >> 3), packs 4 (l & 7) .. + 3 (16 bytes; clamped at the last pack).
-  const uint32_t wvoff = (uint32_t)(lane >> 3) * row_bytes_w +
-                         (uint32_t)min(chunk * kPacks + 4 * (lane & 7), np - 4) * 4u;
-  // X (waves 4..7): rows 16 j .. 16 j + 15; lane l -> row + (l >> 2), slot l & 3
-  // holding granule (l & 3) ^ xswz(row) (16 bytes = 8 f16 columns).
-  const int xw = wave - 4;
+  // W (waves 0..3): wave i moves rows 8 i .. 8 i + 7 of a step. CW = 256:
+  // lane l -> row 8 i + (l >> 3), packs 4 (l & 7) .. + 3 (16 bytes; clamped
+  // at the last pack). CW = 64: lane l -> row 8 i + (l >> 3), pack l & 7.
+  const uint32_t wvoff = CW == 256
+      ? (uint32_t)(lane >> 3) * row_bytes_w + (uint32_t)min(chunk * kPacks + 4 * (lane & 7), np - 4) * 4u
+      : (uint32_t)(lane >> 3) * row_bytes_w + (uint32_t)min(chunk * kPacks + (lane & 7), np - 1) * 4u;
+  // X (waves kXWave0 ..): rows 16 j .. 16 j + 15; lane l -> row + (l >> 2),
+  // slot l & 3 holding granule (l & 3) ^ xswz(row) (16 bytes = 8 f16 columns).
+  const int xw = wave - C::kXWave0;
   const int n_xins = xw < 0 ? 0 : (MT - xw + 3) / 4;  // tiles xw, xw + 4, ... below MT
   uint32_t xvoff[kXPerWave];
 #pragma unroll
@@ -170,30 +216,32 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     const int slot = s % kRing;
     const uint32_t k = (uint32_t)((s0 + s) * kStep);
     if (wave < 4) {
-      dma16(wres, wring + slot * kWSlot + wave * kWBlock, wvoff, (k + 8 * wave) * row_bytes_w);
-    } else {
+      if constexpr (CW == 256) dma16(wres, wring + slot * C::kWSlot + wave * C::kWBlock, wvoff, (k + 8 * wave) * row_bytes_w);
+      else dma4(wres, wring + slot * C::kWSlot + wave * C::kWBlock, wvoff, (k + 8 * wave) * row_bytes_w);
+    }
+    if (xw >= 0) {
 #pragma unroll
       for (int i = 0; i < kXPerWave; ++i)
         if (i < n_xins) dma16(xres, xring + slot * kXSlot + (xw + 4 * i) * 1024, xvoff[i], k * 2u);
     }
   };
-  // VMEM instructions this wave issues per step (uniform per wave).
-  const int per_step = wave < 4 ? 1 : n_xins;
+  // VMEM instructions this wave issues per step (uniform per wave): 1..3.
+  const int per_step = (wave < 4 ? 1 : 0) + n_xins;
   const int pre = min(kRing - 2, steps);
   for (int s = 0; s < pre; ++s) issue(s);
 
-  // ---- per-lane constants: wave w owns packs 4 w .. 4 w + 3 (32 columns, two
-  // 16-column MFMA tiles) for every row tile; in tile t lane lj is pack
-  // 4 w + (lj & 3), packed lane c = 4 t + (lj >> 2) (byte 2 t + (lj >> 3),
-  // nibble (lj >> 2) & 1), so each weight is dequantised once.
-  const int pl = 4 * wave + (lj & 3);  // pack within the chunk
-  const int hh = (lj >> 2) & 1;        // nibble of the byte
+  // ---- per-lane constants: wave w owns packs kPPW w .. kPPW w + kPPW - 1
+  // (16 kT columns) for every row tile; in tile t lane lj is pack
+  // kPPW w + lj % kPPW, packed lane c = (8 / kT) t + lj / kPPW (byte c / 2,
+  // nibble c & 1), so each weight is dequantised once.
+  const int pl = C::kPPW * wave + (lj % C::kPPW);  // pack within the chunk
+  const int hh = (lj / C::kPPW) & 1;               // nibble of the byte
   const bool seq = a.seq != 0;
   int colt[kT];
   uint32_t selt[kT];
 #pragma unroll
   for (int t = 0; t < kT; ++t) {
-    const int c = 4 * t + (lj >> 2);
+    const int c = (8 / kT) * t + lj / C::kPPW;
     colt[t] = seq ? c : awq_col_of_lane(c);
     const uint32_t b = (uint32_t)(c >> 1);
     selt[t] = b | (0x0Cu << 8) | ((4u + b) << 16) | (0x0Cu << 24);
@@ -218,11 +266,11 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   // LDS -> registers for one step: the 8 W words of this lane's pack and the
   // A operands of every row tile.
   auto fetch = [&](int s, uint32_t (&wv)[8], XV (&av)[MT]) {
-    const unsigned char* wsl = wring + (s % kRing) * kWSlot;
+    const unsigned char* wsl = wring + (s % kRing) * C::kWSlot;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int r = 8 * lg + u;
-      wv[u] = *reinterpret_cast<const uint32_t*>(wsl + (r >> 3) * kWBlock + (r & 7) * 128 + pl * 4);
+      wv[u] = *reinterpret_cast<const uint32_t*>(wsl + (r >> 3) * C::kWBlock + (r & 7) * C::kRowBytes + pl * 4);
     }
     const unsigned char* xsl = xring + (s % kRing) * kXSlot;
 #pragma unroll
@@ -233,7 +281,7 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   };
 
   // One step (steps are computed in order): the zero points and scales when
-  // a group starts, then 2 B operands and 2 MT MFMAs.
+  // a group starts, then kT B operands and kT MT MFMAs.
   auto compute = [&](const uint32_t (&wv)[8], const XV (&av)[MT]) {
     if (g_left == 0) {
       ++cur_g;
@@ -245,9 +293,9 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
         const uint32_t zh = __builtin_amdgcn_perm(zw, zw, selt[t]);
         const int col = 8 * pl + colt[t];
         float sv;
-        if (es == 4) sv = reinterpret_cast<const float*>(slds + g * kCols * 4)[col];
-        else if (a.st == AWQ_F16) sv = (float)reinterpret_cast<const f16_t*>(slds + g * kCols * 4)[col];
-        else sv = to_f32(reinterpret_cast<const bf16_t*>(slds + g * kCols * 4)[col]);
+        if (es == 4) sv = reinterpret_cast<const float*>(slds + g * CW * 4)[col];
+        else if (a.st == AWQ_F16) sv = (float)reinterpret_cast<const f16_t*>(slds + g * CW * 4)[col];
+        else sv = to_f32(reinterpret_cast<const bf16_t*>(slds + g * CW * 4)[col]);
         if constexpr (BF) {
           // z s is exact in f32 for 16-bit scales (4 by at most 11 bits).
           const int z = (int)((zh >> (4 * hh)) & 0xFu);
@@ -299,6 +347,7 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     if (s + kRing - 3 < steps) {
       if (per_step == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm((kRing - 4) * 1));
       else if (per_step == 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm((kRing - 4) * 2));
+      else __builtin_amdgcn_s_waitcnt(waitcnt_vm((kRing - 4) * 3));
     } else {
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     }
@@ -309,12 +358,12 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     uint32_t wa[8], wb[8];
     XV xa[MT], xb[MT];
     const bool two = s + 1 < steps;
-    if constexpr (MT <= 3) {
+    if constexpr (MT * kT <= 6) {
       fetch(s, wa, xa);
       if (two) fetch(s + 1, wb, xb);
       compute(wa, xa);
       if (two) compute(wb, xb);
-    } else {  // many row tiles: enough MFMAs per step to cover the LDS latency
+    } else {  // many MFMAs per step: enough to cover the LDS latency
       fetch(s, wa, xa);
       compute(wa, xa);
       if (two) {
@@ -325,8 +374,8 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   }
 
   // ---- epilogue: element r of acc[i][t] is row 16 i + 4 lg + r, column
-  // 8 (chunk*32 + pl) + colt[t] --------------------------------------------------
-  const int nbase = chunk * kCols + 8 * pl;
+  // 8 (chunk kPacks + pl) + colt[t] ----------------------------------------------
+  const int nbase = chunk * CW + 8 * pl;
   if (a.splits > 1) {
     float* part = a.partial + (int64_t)split * a.M * a.N;
 #pragma unroll
@@ -359,16 +408,17 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
     const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
     constexpr int kG = 4, kSB = 4;
-    constexpr int kQuads = kCols / 4;
+    constexpr int kQuads = CW / 4;
+    constexpr int kTh = C::kThreads;
     const int total4 = a.M * kQuads;
-    for (int base = 0; base < total4; base += 512 * kG) {
+    for (int base = 0; base < total4; base += kTh * kG) {
       uint32_t off[kG];
       bool ok[kG];
       float v[kG][4];
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
-        const int e4 = base + g * 512 + tid;
-        const int m = e4 / kQuads, n = chunk * kCols + 4 * (e4 % kQuads);
+        const int e4 = base + g * kTh + tid;
+        const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
         ok[g] = e4 < total4 && n < a.N;
         off[g] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 4)) * 4);
 #pragma unroll
@@ -402,8 +452,8 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
       for (int g = 0; g < kG; ++g) {
         if (!ok[g]) continue;
-        const int e4 = base + g * 512 + tid;
-        const int m = e4 / kQuads, n = chunk * kCols + 4 * (e4 % kQuads);
+        const int e4 = base + g * kTh + tid;
+        const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
@@ -417,18 +467,27 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
     return;
   }
   if constexpr (ACT) {
-    // AutoAWQ order: tiles 0 and 1 of a lane hold packed lanes q and q + 4 of
-    // its pack, i.e. columns 2 q and 2 q + 1 -- a gate/up pair.
+    // AutoAWQ order: packed lanes q and q + 4 of a pack are columns 2 q and
+    // 2 q + 1 -- a gate/up pair. With two tiles per wave they are tiles 0
+    // and 1 of one lane; with one, lanes lj and lj ^ 8 (c = lj / 2).
     const int n = nbase + colt[0];
-    if (n >= a.N) return;
-    const float b0 = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
-    const float b1 = a.bias ? load_f32_any(a.bias, n + 1, a.bt) : 0.f;
 #pragma unroll
     for (int i = 0; i < MT; ++i)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 16 * i + 4 * lg + r;
-        if (m < a.M) store_out(a.y, a.yt, 1, m, n, a.N, acc[i][0][r] + b0, acc[i][1][r] + b1);
+        float g, u;
+        if constexpr (kT == 2) {
+          g = acc[i][0][r];
+          u = acc[i][1][r];
+        } else {
+          g = acc[i][0][r];
+          u = __shfl_xor(g, 8, 64);
+        }
+        const float b0 = (a.bias && n < a.N) ? load_f32_any(a.bias, n, a.bt) : 0.f;
+        const float b1 = (a.bias && n + 1 < a.N) ? load_f32_any(a.bias, n + 1, a.bt) : 0.f;
+        const bool even = kT == 2 || (lj & 8) == 0;
+        if (even && m < a.M && n < a.N) store_out(a.y, a.yt, 1, m, n, a.N, g + b0, u + b1);
       }
     return;
   }
@@ -447,12 +506,13 @@ __global__ __launch_bounds__(512, 1) void skinny_kernel(SkinnyArgs a) {
   }
 }
 
-template <int MT, bool BF>
+template <int MT, bool BF, int CW>
 void launch_mt(const GemmProblem& p) {
+  using C = Chunk<CW>;
   constexpr int kXSlot = 16 * MT * 64;
-  const size_t smem = (size_t)kRing * kWSlot + (size_t)kRing * kXSlot + (size_t)kMaxGroups * kPacks * 4 +
-                      (size_t)kMaxGroups * kCols * 4;
-  const int chunks = (int)((p.N + kCols - 1) / kCols);
+  const size_t smem = (size_t)kRing * C::kWSlot + (size_t)kRing * kXSlot + (size_t)C::kMaxGroups * C::kPacks * 4 +
+                      (size_t)C::kMaxGroups * CW * 4;
+  const int chunks = (int)((p.N + CW - 1) / CW);
   const int total_steps = (int)(p.K / kStep);
   // About one workgroup per CU, each run at least 16 steps and touching at
   // most kMaxGroups groups; fp32 partials (splits x M x N x 4 bytes) at most
@@ -466,7 +526,7 @@ void launch_mt(const GemmProblem& p) {
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, 1024 / p.rows));
   if (int v = tuning(kTuneSkinnySplits, 0); v >= 1) splits = std::min(v, total_steps);
   int sps = (total_steps + splits - 1) / splits;
-  while ((int64_t)sps * kStep / p.group + 2 > kMaxGroups) {
+  while ((int64_t)sps * kStep / p.group + 2 > C::kMaxGroups) {
     ++splits;
     sps = (total_steps + splits - 1) / splits;
   }
@@ -493,42 +553,64 @@ void launch_mt(const GemmProblem& p) {
   a.splits = splits;
   a.steps_per_split = sps;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
+  a.chunks = chunks;
+  // XCD mapping only where grid.x keeps the XCD of a workgroup independent of
+  // its split (chunks % 8 == 0) and each XCD's run covers whole 128-byte lines.
+  a.xcd_chunks = (CW == 64 && chunks % 8 == 0 && (chunks / 8) % 4 == 0) ? chunks : 0;
   if (splits > 1) {
     a.counters = static_cast<uint32_t*>(
         ws_get(p, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));
     a.partial = static_cast<float*>(
         ws_get(p, (size_t)splits * p.rows * p.N * sizeof(float), kWsPartials));
   }
-  ensure_dyn_smem((const void*)skinny_kernel<MT, false, BF>, (int)smem, "hipFuncSetAttribute(skinny)");
-  ensure_dyn_smem((const void*)skinny_kernel<MT, true, BF>, (int)smem, "hipFuncSetAttribute(skinny)");
+  ensure_dyn_smem((const void*)skinny_kernel<MT, false, BF, CW>, (int)smem, "hipFuncSetAttribute(skinny)");
+  ensure_dyn_smem((const void*)skinny_kernel<MT, true, BF, CW>, (int)smem, "hipFuncSetAttribute(skinny)");
   if (p.act)
-    hipLaunchKernelGGL((skinny_kernel<MT, true, BF>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+    hipLaunchKernelGGL((skinny_kernel<MT, true, BF, CW>), dim3(chunks, splits), dim3(C::kThreads), smem, p.stream, a);
   else
-    hipLaunchKernelGGL((skinny_kernel<MT, false, BF>), dim3(chunks, splits), dim3(512), smem, p.stream, a);
+    hipLaunchKernelGGL((skinny_kernel<MT, false, BF, CW>), dim3(chunks, splits), dim3(C::kThreads), smem, p.stream, a);
   check_hip(hipGetLastError(), "skinny kernel launch");
+}
+
+template <bool BF, int CW>
+void launch_rows_cw(const GemmProblem& p) {
+  if (p.rows <= 32) return launch_mt<2, BF, CW>(p);
+  if (p.rows <= 48) return launch_mt<3, BF, CW>(p);
+  if (p.rows <= 64) return launch_mt<4, BF, CW>(p);
+  if (p.rows <= 96) return launch_mt<6, BF, CW>(p);
+  return launch_mt<8, BF, CW>(p);
 }
 
 template <bool BF>
 void launch_rows(const GemmProblem& p) {
-  if (p.rows <= 32) return launch_mt<2, BF>(p);
-  if (p.rows <= 48) return launch_mt<3, BF>(p);
-  if (p.rows <= 64) return launch_mt<4, BF>(p);
-  if (p.rows <= 96) return launch_mt<6, BF>(p);
-  return launch_mt<8, BF>(p);
+  // Chunk width: 256 columns on wide outputs, 64 below 6144 columns. Measured
+  // (us, f16, g128, 64 / 256 columns / large tiles): 4096 -> 4096 at M = 17 /
+  // 64 / 128: 13.6 / 16.0 / 22.0 (15.0 / 22.3 / 36.4; 18.9 / 21.6 / 24.6);
+  // 4096 -> 1024 at M = 32 / 64: 10.0 / 11.5 (15.2 / 20.6; 17.9 / 20.1); but
+  // 4096 -> 14336 at M = 64: 40.0 against 28.9 -- with narrow chunks every
+  // workgroup streams all of X, and wide outputs need no K splits to fill
+  // the CUs anyway. AWQ_SKINNY_COLS=64/256 forces the width.
+  const int cols = tuning(kTuneSkinnyCols, 0);
+  if (cols == 256 || (cols != 64 && p.N >= 6144)) return launch_rows_cw<BF, 256>(p);
+  return launch_rows_cw<BF, 64>(p);
 }
 
 }  // namespace
 
 bool skinny_ok(const GemmProblem& p) {
-  // Where it beats the 128 x 128 split-K tiles of the large-tile kernel
-  // (measured at K 4096..28672, N 1024..28672, 17..128 rows): wide outputs,
-  // whose many column chunks fill the CUs with few K splits (1.1-2.7x at
-  // N >= 6144), and on narrower ones up to 32 rows (1.1-1.5x), or 64 rows
-  // with K >= 8192. 9..16 rows of f16/bf16 also come here instead of the
-  // decode kernels' 16-row tile (f16 0-28 % faster at K 4096..28672,
-  // N 1024..28672; bf16 -8..+20 %). AWQ_SKINNY=0/1 forces the choice.
+  // Where it beats the split-K tiles of the large-tile kernel (measured at
+  // K 4096..28672, N 1024..28672, 17..128 rows): wide outputs (N >= 6144,
+  // 256-column chunks: 1.1-2.7x), and narrower ones (64-column chunks) up to
+  // 128 rows when K <= 8192 and up to 64 rows beyond. 9..16 rows of f16/bf16
+  // also come here instead of the decode kernels' 16-row tile (f16 0-28 %
+  // faster at K 4096..28672, N 1024..28672; bf16 -8..+20 %). AWQ_SKINNY=0/1
+  // forces the choice.
   const int force = tuning(kTuneSkinny, -1);
-  const bool wins = p.N >= 6144 || (p.N >= 1024 && (p.rows <= 32 || (p.rows <= 64 && p.K >= 8192)));
+  // Narrower outputs run 64-column chunks (see launch_rows), which beat the
+  // split-K tiles up to 128 rows when K <= 8192 and up to 64 rows beyond
+  // (14336 -> 4096 at M = 64: 37.7 against 37.6 us; at M = 128 51.3 against
+  // 39.5).
+  const bool wins = p.N >= 6144 || (p.N >= 1024 && (p.K <= 8192 || p.rows <= 64));
   if (force == 0 || (force != 1 && !wins)) return false;
   // bf16 activations need 16-bit scales (z s exact in f32, see the kernel).
   const bool types = p.xt == AWQ_F16 || (p.xt == AWQ_BF16 && p.st != AWQ_F32);

@@ -150,12 +150,14 @@ int awq_gemm_ordered(const void* x, int32_t x_t, const uint32_t* qweight, const 
  * (code under HIP graph capture, serving loops and harnesses that forbid
  * hipMalloc). No counterpart in the reference (whose launcher allocates
  * nothing because it never splits K). Same arguments, constraints, kernels
- * and results as awq_gemm; split-K partial sums and arrival counters go to
- * a static scratch array in device memory (64 MiB per GPU: 1 MiB of
- * counters, 63 MiB of fp32 partials, held by every GPU the library runs on
- * until the process ends) instead of the per-stream workspace. A call whose
- * route needs more partials than that (splits x rows x N x 4 bytes) fails
- * with AWQ_ERR_INVALID before launching anything. The first call on a
+ * and results as awq_gemm; split-K partial sums and arrival counters, and
+ * the f16 hi/lo split of fp32 activations that the fp32 prefill makes, go
+ * to a static scratch array in device memory (128 MiB per GPU: 1 MiB of
+ * counters, 63 MiB of fp32 partials, 64 MiB for the split activations,
+ * M x K x 4 + M x 4 bytes; held by every GPU the library runs on until the
+ * process ends) instead of the per-stream workspace. A call whose route
+ * needs more than a region holds (partials: splits x rows x N x 4 bytes)
+ * fails with AWQ_ERR_INVALID before launching anything. The first call on a
  * device looks the array up (hipGetSymbolAddress) and clears its counters
  * with a kernel on `stream`: make that call outside graph capture. Every
  * call on one GPU shares that GPU's scratch: calls that overlap in time on

@@ -489,15 +489,21 @@ def test_small_m_both_paths(dev, monkeypatch, path, M, x_dt):
     assert oracle.rel_l2(to_host(y), ref) <= tol
 
 
-# fp32 activations at 17..256 rows (and up to 1024 where the launcher's
-# estimate prefers it) run as 16-row slices on the decode kernels' 16-row
-# tile; AWQ_F32_SLICES=0 sends them to the fp32-MFMA prefill kernel, 2 forces
-# slices at any row count. All three, with a ragged last slice (1..15 rows,
-# so also the smaller decode kernels), bias and every output dtype.
-@pytest.mark.parametrize("path", ["1", "0", "2"])
+# fp32 activations past 16 rows: by default the f16 matrix cores with x split
+# into hi + lo (test_f32_prefill_gpu.py covers that route in depth);
+# AWQ_F32_SLICES=2 runs 16-row slices of the decode kernels' 16-row tile, and
+# AWQ_GEMM_TILE=1 with AWQ_F32_SLICES=0 the generic fp32-MFMA kernel. All
+# three, with a ragged last slice (1..15 rows, so also the smaller decode
+# kernels), bias and every output dtype.
+F32_PATHS = {"default": {}, "slices": {"AWQ_F32_SLICES": "2"},
+             "generic": {"AWQ_F32_SLICES": "0", "AWQ_GEMM_TILE": "1"}}
+
+
+@pytest.mark.parametrize("path", list(F32_PATHS))
 @pytest.mark.parametrize("M,y_dt", [(17, "f32"), (33, "f16"), (100, "bf16"), (256, "f32"), (300, "f32")])
 def test_f32_rows_slices_and_prefill_kernel(dev, monkeypatch, path, M, y_dt):
-    monkeypatch.setenv("AWQ_F32_SLICES", path)
+    for k, v in F32_PATHS[path].items():
+        monkeypatch.setenv(k, v)
     K, N, g = 1024, 1056, 64
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f32", s_dt="f16", bias=True)
     y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f32", "f16", y_dt))
@@ -517,23 +523,31 @@ def test_small_m_every_configuration(dev, monkeypatch, rpw):
 
 
 # 9..128 rows of f16 or bf16 activations (16-bit scales) run on the skinny
-# kernel (awq_skinny.hip); AWQ_SKINNY=0 sends them to the large-tile kernels
-# (17..128 rows) or the 16-row decode tile (9..16).
-@pytest.mark.parametrize("path", ["1", "0"])
+# kernel (awq_skinny.hip), in 64- or 256-column chunks; AWQ_SKINNY=0 sends
+# them to the large-tile kernels (17..128 rows) or the 16-row decode tile
+# (9..16).
+SKINNY_PATHS = {"c64": {"AWQ_SKINNY": "1", "AWQ_SKINNY_COLS": "64"},
+                "c256": {"AWQ_SKINNY": "1", "AWQ_SKINNY_COLS": "256"}, "off": {"AWQ_SKINNY": "0"}}
+
+
+@pytest.mark.parametrize("path", list(SKINNY_PATHS))
 @pytest.mark.parametrize("M", [9, 16, 17, 33, 48, 64, 80, 96, 100, 128])
 @pytest.mark.parametrize("x_dt", ["f16", "bf16"])
 def test_skinny_both_paths(dev, monkeypatch, path, M, x_dt):
-    monkeypatch.setenv("AWQ_SKINNY", path)
+    for k, v in SKINNY_PATHS[path].items():
+        monkeypatch.setenv(k, v)
     K, N, g = 2048, 2080, 128  # N % 256 != 0: ragged last chunk
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=x_dt, bias=True)
     y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, x_dt, "f32")
     assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, x_dt, x_dt)) <= TOL_MFMA
 
 
+@pytest.mark.parametrize("cols", ["64", "256"])
 @pytest.mark.parametrize("splits", [1, 3, 8, 64])
 @pytest.mark.parametrize("x_dt,s_dt,g", [("f16", "f16", 64), ("f16", "f32", 128), ("f16", "bf16", 256),
                                          ("bf16", "bf16", 64), ("bf16", "f16", 128)])
-def test_skinny_every_split(dev, monkeypatch, splits, x_dt, s_dt, g):
+def test_skinny_every_split(dev, monkeypatch, cols, splits, x_dt, s_dt, g):
+    monkeypatch.setenv("AWQ_SKINNY_COLS", cols)
     monkeypatch.setenv("AWQ_SKINNY_SPLITS", str(splits))
     M, K, N = 48, 4096, 768
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
@@ -544,15 +558,17 @@ def test_skinny_every_split(dev, monkeypatch, splits, x_dt, s_dt, g):
     assert oracle.rel_l2(host_f32(y, y_dt), _ref64(x, qw, qz, sc, b, g, x_dt, s_dt)) <= TOL_MFMA
 
 
+@pytest.mark.parametrize("cols", ["64", "256"])
 @pytest.mark.parametrize("M", [12, 48, 128])
 @pytest.mark.parametrize("splits", ["1", "3"])
 @pytest.mark.parametrize("x_dt,s_dt", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f16"), ("f16", "bf16")])
-def test_skinny_weights_exact(dev, monkeypatch, M, splits, x_dt, s_dt):
+def test_skinny_weights_exact(dev, monkeypatch, cols, M, splits, x_dt, s_dt):
     """Each row of X selects one k (a single 1), so row m of Y is row k_m of
     the weights as the kernel dequantised them, with nothing else added:
     bit-exact against (q - z) * s rounded once to the activation type (the
     reference's F-typed dequant, src/kernel/awq_kernel_gemm.rs:181-439)."""
     monkeypatch.setenv("AWQ_SKINNY", "1")
+    monkeypatch.setenv("AWQ_SKINNY_COLS", cols)
     monkeypatch.setenv("AWQ_SKINNY_SPLITS", splits)
     K, N, g = 2048, 768, 128
     _, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt)
@@ -564,3 +580,18 @@ def test_skinny_weights_exact(dev, monkeypatch, M, splits, x_dt, s_dt):
     w32 = oracle.dequant(qw, qz, host_f32(sc, s_dt), g, order="awq")  # exact for 16-bit scales
     want = host_f32(round_to(w32[ks], x_dt), x_dt)
     assert np.array_equal(y, want)
+
+
+@pytest.mark.parametrize("M,K,N", [(64, 4096, 4096), (17, 4096, 14336), (100, 2048, 2048), (40, 14336, 4096)])
+@pytest.mark.parametrize("splits", ["0", "1", "3"])
+def test_skinny_narrow_chunks_xcd_mapped(dev, monkeypatch, M, K, N, splits):
+    # 64-column chunks on outputs whose chunk count lets each XCD run a
+    # contiguous run of them (N % 2048 == 0), with and without K splits.
+    monkeypatch.setenv("AWQ_SKINNY", "1")
+    monkeypatch.setenv("AWQ_SKINNY_COLS", "64")
+    if splits != "0":
+        monkeypatch.setenv("AWQ_SKINNY_SPLITS", splits)
+    g = 128
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt="f16", s_dt="f16", bias=True)
+    y = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, "f16", "f16", "f32")
+    assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, "f16", "f16")) <= TOL_MFMA

@@ -68,7 +68,12 @@ ROUTES = [
     (300, "bf16", {}),
     (300, "f16", {"AWQ_GEMM_TILE": "1"}),             # generic tiles
     (300, "f16", {"AWQ_GEMM_TILE": "10"}),            # 256 x 224 tiles, ping-pong halves
-    (40, "f32", {}),                                  # fp32 prefill
+    (40, "f32", {}),                                  # fp32 prefill: x split hi + lo, matrix cores
+    (200, "f32", {"AWQ_GEMM_TILE": "4"}),             # the same on 128 x 128 tiles
+    (20, "f32", {}),                                  # fp32, 16-row slices
+    (64, "f16", {"AWQ_SKINNY_COLS": "256", "AWQ_SKINNY_SPLITS": "1"}),  # 256-column skinny, direct store
+    (64, "f16", {"AWQ_SKINNY_COLS": "256"}),          # 256-column skinny, split-K
+    (96, "bf16", {"AWQ_SKINNY": "1", "AWQ_SKINNY_COLS": "256", "AWQ_SKINNY_SPLITS": "1"}),
 ]
 
 
