@@ -1113,6 +1113,59 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
       __hip_atomic_store(&a.counters[t * kTileCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
+  if constexpr (!ACT) {
+    // The tile goes through LDS (idle now) so that Y is written in 16-byte
+    // pieces of whole rows. Stored straight from the MFMA layout, a wave's
+    // store instruction covers 16 or 32 columns of several rows, pieces of
+    // 128-byte lines that were each written back in parts (HBM writes 1.75x
+    // the output bytes at 2048 x 4096 -> 14336 with f16 output; staged: 1.0x,
+    // 240 -> 222 us). Rows of the staged tile are BN * es + 16 bytes apart
+    // (bank spread); an f32 tile that does not fit goes in row passes.
+    auto staged = [&](auto es_c) {
+      constexpr int es = decltype(es_c)::value;
+      constexpr int pitch = BN * es + 16;
+      constexpr int rows_pass = ((int)(C::kSmem / pitch) & ~(MS - 1)) < BM ? ((int)(C::kSmem / pitch) & ~(MS - 1)) : BM;
+      constexpr int gran = BN * es / 16;  // 16-byte pieces per tile row
+      static_assert(rows_pass >= MS, "staged rows");
+      char* yb = static_cast<char*>(a.y);
+      for (int p0 = 0; p0 < BM; p0 += rows_pass) {
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < C::kJ; ++j) {
+          const int n = out_col(j);
+          const float bias = (a.bias && n < a.N) ? load_f32_any(a.bias, n, a.bt) : 0.f;
+          const int lc = n - n0;
+#pragma unroll
+          for (int i = 0; i < C::kI; ++i) {
+#pragma unroll
+            for (int r = 0; r < kAccN; ++r) {
+              const int lr = out_row(i, r) - m0 - p0;
+              if (rows_pass < BM && (lr < 0 || lr >= rows_pass)) continue;
+              const float v = acc[i][j][r] + bias;
+              unsigned char* d = smem_raw + lr * pitch + lc * es;
+              if constexpr (es == 4) *reinterpret_cast<float*>(d) = v;
+              else if (a.yt == AWQ_BF16) *reinterpret_cast<bf16_t*>(d) = from_f32<bf16_t>(v);
+              else *reinterpret_cast<f16_t*>(d) = from_f32<f16_t>(v);
+            }
+          }
+        }
+        __syncthreads();
+        const int rows = min(rows_pass, BM - p0);
+        for (int g = tid; g < rows * gran; g += C::kThreads) {
+          const int row = g / gran, gc = g % gran;
+          const int m = m0 + p0 + row;
+          const int n = n0 + gc * 16 / es;  // N % 32 == 0: a piece is all in or all out
+          const u32x4 v = *reinterpret_cast<const u32x4*>(smem_raw + row * pitch + gc * 16);
+          if (m < a.M && n < a.N) *reinterpret_cast<u32x4*>(yb + ((int64_t)m * a.N + n) * es) = v;
+        }
+      }
+    };
+    // LDS-direct prefetches of clamped tail stages may still be landing.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (a.yt == AWQ_F32) staged(std::integral_constant<int, 4>{});
+    else staged(std::integral_constant<int, 2>{});
+    return;
+  }
   // Column lane % 32 (or % 16): a gate/up pair is this lane and its xor-1
   // neighbour (N is even, so both are in range or neither).
 #pragma unroll
