@@ -137,6 +137,36 @@ constexpr int kCachePolicyNT = 2;
 // Device-coherent (agent scope) access: sc1, as agent-scope atomic loads and
 // stores use, so data written by other workgroups' sc1 stores is seen.
 constexpr int kCachePolicySC1 = 16;
+
+// Split-K handshake (decode, skinny and large-tile kernels). Each workgroup
+// of a K split writes its fp32 partials, then counts its arrival on a
+// per-chunk counter; the workgroup that arrives last sums every split's
+// partials and re-arms the counter. Why relaxed agent-scope atomics and a
+// vmcnt wait are enough, without the L2 writeback / invalidate that a
+// release / acquire pair would add on gfx950 (one L2 per XCD):
+//  * Writer. Every partial is stored with an agent-scope atomic store (sc1),
+//    which is written through its XCD's L2 to the device's point of
+//    coherence instead of staying dirty there; that writeback is what an
+//    agent-scope release adds, for plain stores only. Each wave then waits
+//    for its stores to complete (s_waitcnt vmcnt(0): a store's count drops
+//    once the write is acknowledged at its scope), and a workgroup barrier
+//    follows, so every partial of the workgroup is visible device-wide
+//    before thread 0 issues the counter's fetch_add. The asm statement's
+//    "memory" clobber and the barrier also keep the compiler from moving
+//    the stores past the fetch_add.
+//  * Reader. Only the workgroup whose fetch_add returned splits - 1 reads
+//    the partials, and its loads are issued after that value has returned
+//    (a barrier and a branch on it). They are agent-scope atomic loads, or
+//    buffer loads with the same sc1 policy (kCachePolicySC1), which do not
+//    return a stale line of this XCD's L2; the invalidate an agent-scope
+//    acquire adds is for plain loads only. The reader never reads partials
+//    it did not wait for, since every writer's fetch_add follows its
+//    stores.
+//  * Re-arm. The last workgroup stores 0 to the counter; the next call on
+//    the stream starts after this kernel ends (stream order), so no
+//    arrival of the next call races with the reset.
+// The counters are zeroed once when their buffer is allocated and are back
+// at zero after every complete launch.
 __device__ __forceinline__ uint32_t buf_load_u32_nt(rsrc_t r, uint32_t voff, uint32_t soff) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, kCachePolicyNT);
 }

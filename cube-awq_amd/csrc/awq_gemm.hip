@@ -1035,6 +1035,7 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
         }
       }
     }
+    // Partials complete before the arrival (split-K handshake, awq_common.h).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     // The flag lives in the (now idle) tile buffers: a static __shared__
     // variable would push the 160 KB configuration over the LDS limit.

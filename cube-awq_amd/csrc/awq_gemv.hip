@@ -291,12 +291,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
 
   const int col_base = chunk * kChunkCols;
   if (a.splits > 1) {
-    // Cross-workgroup handshake without an L2 writeback/invalidate: partials
-    // are written with agent-scope (write-through, sc1) stores, the wave waits
-    // for their completion (vmcnt 0), and only then the workgroup's arrival is
-    // counted. The last workgroup to arrive for this chunk reads all partials
-    // with agent-scope (sc1) loads, sums them in split order, and re-arms the
-    // counter for the next call.
+    // Split-K handshake (the memory-ordering argument is in awq_common.h):
+    // partials written with agent-scope (write-through, sc1) stores, the wave
+    // waits for their completion (vmcnt 0), and only then the workgroup's
+    // arrival is counted. The last workgroup to arrive for this chunk reads
+    // all partials with agent-scope (sc1) loads, sums them in split order,
+    // and re-arms the counter for the next call.
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int o = threadIdx.x + i * 64 * WAVES;
@@ -305,6 +305,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
         __hip_atomic_store(&a.partial[((int64_t)split * MT + m) * a.N + col_base + c], res[i],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // Partials complete before the arrival (split-K handshake, awq_common.h).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -461,6 +462,7 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*re
         __hip_atomic_store(&a.partial[((int64_t)split * MV + m) * a.N + col_base + c], res[i],
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    // Partials complete before the arrival (split-K handshake, awq_common.h).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0) {

@@ -390,6 +390,7 @@ __global__ __launch_bounds__(Chunk<CW>::kThreads) void skinny_kernel(SkinnyArgs 
             __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][t][r], __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         }
+    // Partials complete before the arrival (split-K handshake, awq_common.h).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     volatile int* s_last = reinterpret_cast<volatile int*>(smem);  // ring is idle now
     __syncthreads();
