@@ -144,8 +144,10 @@ constexpr int kCachePolicySC1 = 16;
 // partials and re-arms the counter. Why relaxed agent-scope atomics and a
 // vmcnt wait are enough, without the L2 writeback / invalidate that a
 // release / acquire pair would add on gfx950 (one L2 per XCD):
-//  * Writer. Every partial is stored with an agent-scope atomic store (sc1),
-//    which is written through its XCD's L2 to the device's point of
+//  * Writer. Every partial is stored with an agent-scope atomic store or a
+//    buffer store with the same sc1 policy (kCachePolicySC1; 16-byte pieces
+//    where the partials are staged through LDS), which is written through
+//    its XCD's L2 to the device's point of
 //    coherence instead of staying dirty there; that writeback is what an
 //    agent-scope release adds, for plain stores only. Each wave then waits
 //    for its stores to complete (s_waitcnt vmcnt(0): a store's count drops

@@ -81,6 +81,14 @@ struct Chunk {
   static_assert(kT >= 1 && kPPW * kWaves == kPacks, "chunk layout");
 };
 
+// Dynamic LDS of skinny_kernel<MT, *, *, CW>: the W and X rings, then the
+// zero words and scales of up to kMaxGroups groups.
+template <int MT, int CW>
+constexpr int skinny_smem_bytes() {
+  return kRing * Chunk<CW>::kWSlot + kRing * 16 * MT * 64 + Chunk<CW>::kMaxGroups * Chunk<CW>::kPacks * 4 +
+         Chunk<CW>::kMaxGroups * CW * 4;
+}
+
 struct SkinnyArgs {
   const void* x;
   const uint32_t* qweight;
@@ -127,6 +135,7 @@ __global__ __launch_bounds__(Chunk<CW>::kThreads) void skinny_kernel(SkinnyArgs 
   // 16-byte DMAs per step for X: rows 16 j .. 16 j + 15 by X wave j % 4.
   constexpr int kXPerWave = (MT + 3) / 4;
   static_assert(MT >= 2 && MT <= 8, "row tiles");
+  constexpr int kSmem = skinny_smem_bytes<MT, CW>();
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* wring = smem;                               // kRing W slots
   unsigned char* xring = smem + kRing * C::kWSlot;           // kRing X slots
@@ -377,22 +386,58 @@ __global__ __launch_bounds__(Chunk<CW>::kThreads) void skinny_kernel(SkinnyArgs 
   // 8 (chunk kPacks + pl) + colt[t] ----------------------------------------------
   const int nbase = chunk * CW + 8 * pl;
   if (a.splits > 1) {
-    float* part = a.partial + (int64_t)split * a.M * a.N;
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
+    constexpr int kQuads = CW / 4;
+    // 256-column chunks stage the partial tile in LDS (idle once every wave
+    // has left the main loop) and store it as whole 16-byte row pieces with
+    // the agent-scope (sc1) policy: full 128-byte lines instead of 4-byte
+    // stores scattered over the MFMA layout, which wrote each line in halves
+    // (4096 -> 14336 at M = 64: the store phase 4.9 -> 2.4 us, the call
+    // 29.8 -> 26.7 us; M = 128 44.9 -> 39.4 us). 64-column chunks keep the
+    // direct stores (staged, 4096 -> 4096 at M = 64 measured 15.6 -> 16.8 us;
+    // reading the own split back from LDS in the sum was slower too).
+    constexpr bool kStage = CW == 256;
+    constexpr int kPitch = CW * 4 + 16;  // bytes per staged row (the pad spreads the banks)
+    static_assert(!kStage || 16 * MT * kPitch + 16 <= kSmem, "the partial tile fits the LDS");
+    volatile int* s_last = reinterpret_cast<volatile int*>(smem + kSmem - 16);  // past the staged tile
+    if constexpr (kStage) {
+      __syncthreads();  // every wave is done with the ring
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
+      for (int i = 0; i < MT; ++i)
 #pragma unroll
-      for (int t = 0; t < kT; ++t)
+        for (int t = 0; t < kT; ++t)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * i + 4 * lg + r;
-          const int n = nbase + colt[t];
-          if (m < a.M && n < a.N)
-            __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][t][r], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+          for (int r = 0; r < 4; ++r)
+            *reinterpret_cast<float*>(smem + (16 * i + 4 * lg + r) * kPitch + (8 * pl + colt[t]) * 4) =
+                acc[i][t][r];
+      __syncthreads();
+      const uint32_t split_off = (uint32_t)((int64_t)split * a.M * a.N * 4);
+      for (int e = tid; e < a.M * kQuads; e += C::kThreads) {
+        const int m = e / kQuads, q = e % kQuads;
+        const int n = chunk * CW + 4 * q;
+        if (n < a.N) {
+          const u32x4_t v = *reinterpret_cast<const u32x4_t*>(smem + m * kPitch + q * 16);
+          __builtin_amdgcn_raw_buffer_store_b128(v, pres, (uint32_t)(((int64_t)m * a.N + n) * 4), split_off,
+                                                 kCachePolicySC1);
         }
+      }
+    } else {
+      float* part = a.partial + (int64_t)split * a.M * a.N;
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int t = 0; t < kT; ++t)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = 16 * i + 4 * lg + r;
+            const int n = nbase + colt[t];
+            if (m < a.M && n < a.N)
+              __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][t][r], __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+          }
+    }
     // Partials complete before the arrival (split-K handshake, awq_common.h).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    volatile int* s_last = reinterpret_cast<volatile int*>(smem);  // ring is idle now
     __syncthreads();
     if (tid == 0) {
       const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCtrStride], 1u, __ATOMIC_RELAXED,
@@ -406,10 +451,8 @@ __global__ __launch_bounds__(Chunk<CW>::kThreads) void skinny_kernel(SkinnyArgs 
     // per thread per round, kSB splits deep -- kG kSB loads in flight, so
     // most chunks take one round. Slots past the chunk, M or the splits are
     // loaded clamped and not used.
-    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
     const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
     constexpr int kG = 4, kSB = 4;
-    constexpr int kQuads = CW / 4;
     constexpr int kTh = C::kThreads;
     const int total4 = a.M * kQuads;
     for (int base = 0; base < total4; base += kTh * kG) {
@@ -510,9 +553,7 @@ __global__ __launch_bounds__(Chunk<CW>::kThreads) void skinny_kernel(SkinnyArgs 
 template <int MT, bool BF, int CW>
 void launch_mt(const GemmProblem& p) {
   using C = Chunk<CW>;
-  constexpr int kXSlot = 16 * MT * 64;
-  const size_t smem = (size_t)kRing * C::kWSlot + (size_t)kRing * kXSlot + (size_t)C::kMaxGroups * C::kPacks * 4 +
-                      (size_t)C::kMaxGroups * CW * 4;
+  const size_t smem = (size_t)skinny_smem_bytes<MT, CW>();
   const int chunks = (int)((p.N + CW - 1) / CW);
   const int total_steps = (int)(p.K / kStep);
   // About one workgroup per CU, each run at least 16 steps and touching at
