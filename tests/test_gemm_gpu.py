@@ -523,11 +523,17 @@ def test_small_m_every_configuration(dev, monkeypatch, rpw):
 
 
 # 9..128 rows of f16 or bf16 activations (16-bit scales) run on the skinny
-# kernel (awq_skinny.hip), in 64- or 256-column chunks; AWQ_SKINNY=0 sends
-# them to the large-tile kernels (17..128 rows) or the 16-row decode tile
-# (9..16).
+# kernel (awq_skinny.hip), in 64-column chunks (4 waves) or 256-column chunks
+# (8 waves); AWQ_SKINNY=0 sends them to the large-tile kernels (17..128 rows)
+# or the 16-row decode tile (9..16).
 SKINNY_PATHS = {"c64": {"AWQ_SKINNY": "1", "AWQ_SKINNY_COLS": "64"},
                 "c256": {"AWQ_SKINNY": "1", "AWQ_SKINNY_COLS": "256"}, "off": {"AWQ_SKINNY": "0"}}
+SKINNY_COLS = {"64": SKINNY_PATHS["c64"], "256": SKINNY_PATHS["c256"]}
+
+
+def _skinny_cols(monkeypatch, cols):
+    for k, v in SKINNY_COLS[cols].items():
+        monkeypatch.setenv(k, v)
 
 
 @pytest.mark.parametrize("path", list(SKINNY_PATHS))
@@ -542,12 +548,12 @@ def test_skinny_both_paths(dev, monkeypatch, path, M, x_dt):
     assert oracle.rel_l2(to_host(y), _ref64(x, qw, qz, sc, b, g, x_dt, x_dt)) <= TOL_MFMA
 
 
-@pytest.mark.parametrize("cols", ["64", "256"])
+@pytest.mark.parametrize("cols", list(SKINNY_COLS))
 @pytest.mark.parametrize("splits", [1, 3, 8, 64])
 @pytest.mark.parametrize("x_dt,s_dt,g", [("f16", "f16", 64), ("f16", "f32", 128), ("f16", "bf16", 256),
                                          ("bf16", "bf16", 64), ("bf16", "f16", 128)])
 def test_skinny_every_split(dev, monkeypatch, cols, splits, x_dt, s_dt, g):
-    monkeypatch.setenv("AWQ_SKINNY_COLS", cols)
+    _skinny_cols(monkeypatch, cols)
     monkeypatch.setenv("AWQ_SKINNY_SPLITS", str(splits))
     M, K, N = 48, 4096, 768
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
@@ -558,7 +564,7 @@ def test_skinny_every_split(dev, monkeypatch, cols, splits, x_dt, s_dt, g):
     assert oracle.rel_l2(host_f32(y, y_dt), _ref64(x, qw, qz, sc, b, g, x_dt, s_dt)) <= TOL_MFMA
 
 
-@pytest.mark.parametrize("cols", ["64", "256"])
+@pytest.mark.parametrize("cols", list(SKINNY_COLS))
 @pytest.mark.parametrize("M", [12, 48, 128])
 @pytest.mark.parametrize("splits", ["1", "3"])
 @pytest.mark.parametrize("x_dt,s_dt", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f16"), ("f16", "bf16")])
@@ -567,8 +573,7 @@ def test_skinny_weights_exact(dev, monkeypatch, cols, M, splits, x_dt, s_dt):
     the weights as the kernel dequantised them, with nothing else added:
     bit-exact against (q - z) * s rounded once to the activation type (the
     reference's F-typed dequant, src/kernel/awq_kernel_gemm.rs:181-439)."""
-    monkeypatch.setenv("AWQ_SKINNY", "1")
-    monkeypatch.setenv("AWQ_SKINNY_COLS", cols)
+    _skinny_cols(monkeypatch, cols)
     monkeypatch.setenv("AWQ_SKINNY_SPLITS", splits)
     K, N, g = 2048, 768, 128
     _, qw, qz, sc, _ = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt)

@@ -76,9 +76,12 @@ def test_sequential_every_tile_configuration(dev, monkeypatch, tile, dt):
 
 @pytest.mark.parametrize("M", [17, 64, 128])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-def test_sequential_skinny_kernel(dev, monkeypatch, M, dt):
+@pytest.mark.parametrize("chunk", [{}, {"AWQ_SKINNY_COLS": "256"}])
+def test_sequential_skinny_kernel(dev, monkeypatch, M, dt, chunk):
     """17..128 rows of f16 or bf16 on the skinny kernel, forced on at a narrow N."""
     monkeypatch.setenv("AWQ_SKINNY", "1")
+    for k, v in chunk.items():
+        monkeypatch.setenv(k, v)
     K, N, g = 2048, 2080, 128
     x, qw_awq, qz_awq, sc, b = make_problem(M, K, N, g, x_dt=dt, s_dt=dt, bias=True)
     qw_seq, qz_seq = _to_seq(qw_awq), _to_seq(qz_awq)

@@ -73,6 +73,7 @@ ROUTES = [
     (20, "f32", {}),                                  # fp32, 16-row slices
     (64, "f16", {"AWQ_SKINNY_COLS": "256", "AWQ_SKINNY_SPLITS": "1"}),  # 256-column skinny, direct store
     (64, "f16", {"AWQ_SKINNY_COLS": "256"}),          # 256-column skinny, split-K
+    (48, "bf16", {"AWQ_SKINNY_COLS": "256", "AWQ_SKINNY_SPLITS": "1"}),  # 256-column bf16, direct store
     (96, "bf16", {"AWQ_SKINNY": "1", "AWQ_SKINNY_COLS": "256", "AWQ_SKINNY_SPLITS": "1"}),
 ]
 
