@@ -1364,7 +1364,12 @@ void launch_mode(const GemmProblem& p) {
     };
     if (tiles(256, 224) >= 240 && 0.85 * waves(tiles(256, 224)) < waves(tiles(256, 256))) cfg = 10;
     else if (tiles(256, 256) >= 240) cfg = 2;
-    else if (tiles(128, 256) >= 200) cfg = 3;
+    // 128 x 256 tiles run 16x16x32 MFMA blocks (12): against 32x32x16 (3)
+    // 2048 x 4096 -> 4096 82.5 -> 78.4 us, 2048 x 14336 -> 4096 265 -> 254 us,
+    // 0-4 % faster on 11 of 12 split-K shapes at M = 129..1024 (the 12th,
+    // 768 x 4096 -> 6144, 1.3 % slower); a ping-pong 128 x 256 (11) was not
+    // faster than 3.
+    else if (tiles(128, 256) >= 200) cfg = 12;
     else {
       cfg = 4;  // 128 x 128 tiles, two workgroups per CU
       const int64_t t = tiles(128, 128);
@@ -1396,7 +1401,7 @@ void launch_mode(const GemmProblem& p) {
         const int64_t cus = device_cus();
         const int64_t waves4 = (t * splits + cus - 1) / cus, waves3 = (t3 * s3 + cus - 1) / cus;
         if (2 * waves3 * splits <= waves4 * s3 && (s3 <= 4 || stages / s3 >= 16)) {
-          cfg = 3;
+          cfg = 12;
           splits = s3;
         }
       }
@@ -1437,7 +1442,8 @@ void launch_mode(const GemmProblem& p) {
     // X tiles hold hi and lo rows, so 256-row tiles do not fit the LDS: the
     // 128 x 256 tile (8 waves) where a 256-row or wide tile was chosen,
     // else 128 x 128 (4 waves), with the split count chosen above.
-    if (cfg == 3 || cfg == 2 || cfg == 6 || cfg == 7 || cfg == 8 || cfg == 9 || cfg == 10)
+    if (cfg == 3 || cfg == 2 || cfg == 6 || cfg == 7 || cfg == 8 || cfg == 9 || cfg == 10 || cfg == 11 ||
+        cfg == 12)
       return launch_big<MODE, ST, 128, 256, 2, 4, 32, SEQ>(p, splits);
     return launch_big<MODE, ST, 128, 128, 2, 2, 32, SEQ>(p, splits);
   } else if constexpr (MODE != MODE_F32) {
@@ -1450,6 +1456,8 @@ void launch_mode(const GemmProblem& p) {
       case 8: return launch_big<MODE, ST, 64, 256, 1, 8, 32, SEQ>(p, splits);
       case 9: return launch_big<MODE, ST, 256, 224, 4, 2, 16, SEQ>(p, splits);  // single-phase
       case 10: return launch_big<MODE, ST, 256, 224, 4, 2, 16, SEQ, true>(p, splits);  // ping-pong
+      case 11: return launch_big<MODE, ST, 128, 256, 2, 4, 16, SEQ, true>(p, splits);  // ping-pong
+      case 12: return launch_big<MODE, ST, 128, 256, 2, 4, 16, SEQ>(p, splits);  // single-phase
       default: break;
     }
   }

@@ -325,7 +325,7 @@ def test_repeated_calls_bit_identical(dev, M):
         assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("splits", [1, 3, 8])
 @pytest.mark.parametrize("x_dt", ["f16", "bf16"])
 def test_prefill_every_tile_configuration(dev, monkeypatch, tile, splits, x_dt):
@@ -342,18 +342,20 @@ def test_prefill_every_tile_configuration(dev, monkeypatch, tile, splits, x_dt):
     assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_MFMA
 
 
+@pytest.mark.parametrize("tiles", [(9, 10), (12, 11)])
 @pytest.mark.parametrize("splits", [1, 3])
 @pytest.mark.parametrize("x_dt,s_dt", [("f16", "f16"), ("bf16", "bf16"), ("f16", "f32")])
-def test_prefill_ping_pong_matches_single_phase_bits(dev, monkeypatch, splits, x_dt, s_dt):
-    """The 256 x 224 tile with the two halves of its waves a phase apart
-    (tile 10) performs each accumulator's MFMAs in the same order as the
-    single-phase schedule (tile 9), so the outputs are bit-identical; checked
-    on a shape ragged in M and N, 12 stages, with and without K splits."""
+def test_prefill_ping_pong_matches_single_phase_bits(dev, monkeypatch, tiles, splits, x_dt, s_dt):
+    """The 256 x 224 and 128 x 256 tiles with the two halves of their waves a
+    phase apart (tiles 10, 11) perform each accumulator's MFMAs in the same
+    order as the single-phase schedule (tiles 9, 12), so the outputs are
+    bit-identical; checked on a shape ragged in M and N, 12 stages, with and
+    without K splits."""
     monkeypatch.setenv("AWQ_GEMM_SPLITS", str(splits))
     M, K, N, g = 520, 768, 1120, 64
     x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
     outs = []
-    for tile in (9, 10):
+    for tile in tiles:
         monkeypatch.setenv("AWQ_GEMM_TILE", str(tile))
         outs.append(to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, "f32")))
     assert np.isfinite(outs[1]).all()

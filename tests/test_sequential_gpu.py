@@ -60,7 +60,7 @@ def test_sequential_matches_oracle_and_autoawq_bits(dev, M, dt):
     assert oracle.rel_l2(y_seq, ref) <= tol
 
 
-@pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 def test_sequential_every_tile_configuration(dev, monkeypatch, tile, dt):
     monkeypatch.setenv("AWQ_GEMM_TILE", str(tile))
