@@ -554,15 +554,15 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
   const int kc = live ? k0 : 0;
   const int grp = kc / a.group;
 
-  // ---- loads: the wave's RPW weight rows first, then the zero words and
-  // scales of the 4 packs this lane feeds (pack chunk*64 + 16 s + lj), then
-  // its activations.
-  const rsrc_t wr = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
-  const uint32_t voff = (uint32_t)pack_c * 4u;
-  const uint32_t row_bytes = (uint32_t)np * 4u;
-  uint32_t w[RPW];
+  // ---- loads: the activations, then the zero words and scales of the 4
+  // packs this lane feeds (pack chunk*64 + 16 s + lj), then the wave's RPW
+  // weight rows (activations first: 16 rows at 4096 -> 14336 23.9 -> 23.3 us).
+  // A operand: lane (lg, lj) holds x[lj, k + 8 lg .. k + 8 lg + 7] of each step.
+  const bool xrow_ok = lj < rows;
+  const int64_t xbase = (int64_t)min(lj, rows - 1) * a.K + kc + 8 * lg;
+  float xv[kSteps][8];
 #pragma unroll
-  for (int r = 0; r < RPW; ++r) w[r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + r) * row_bytes);
+  for (int b = 0; b < kSteps; ++b) load_x8<XT>(a.x, xbase + 32 * b, xv[b]);
   uint32_t zq[4];
   RawScales sraw[4];
 #pragma unroll
@@ -571,16 +571,20 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
     zq[s] = a.qzeros[(int64_t)grp * np + pk];
     sraw[s] = load_scales_raw(a.scales, a.st, (int64_t)grp * a.N + (int64_t)pk * 8);
   }
-  // A operand: lane (lg, lj) holds x[lj, k + 8 lg .. k + 8 lg + 7] of each step.
-  const bool xrow_ok = lj < rows;
-  const int64_t xbase = (int64_t)min(lj, rows - 1) * a.K + kc + 8 * lg;
-  float xv[kSteps][8];
+  // Issued before the weight rows (a compiler barrier: otherwise the row
+  // mask below turns the activation loads into predicated loads placed
+  // after the weights, and the activations' row scale waits for every row).
+  asm volatile("" ::: "memory");
+  const rsrc_t wr = make_rsrc(a.qweight, (uint32_t)a.K * (uint32_t)np * 4u);
+  const uint32_t voff = (uint32_t)pack_c * 4u;
+  const uint32_t row_bytes = (uint32_t)np * 4u;
+  uint32_t w[RPW];
 #pragma unroll
-  for (int b = 0; b < kSteps; ++b) {
-    load_x8<XT>(a.x, xbase + 32 * b, xv[b]);
+  for (int r = 0; r < RPW; ++r) w[r] = buf_load_u32_nt(wr, voff, (uint32_t)(kc + r) * row_bytes);
+#pragma unroll
+  for (int b = 0; b < kSteps; ++b)
 #pragma unroll
     for (int e = 0; e < 8; ++e) xv[b][e] = xrow_ok ? xv[b][e] : 0.f;
-  }
   // Row scale (not for f16 activations, which are exact as they are): the
   // largest |x| of row lj over this wave's rows goes to [2^14, 2^15).
   float xdown[4] = {1.f, 1.f, 1.f, 1.f};  // undo factor of D rows 4 lg + r
@@ -615,79 +619,86 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_mfma_kernel(GemvArgs a) {
       alo[b][e] = (_Float16)(xv[b][e] - (float)h);
     }
 
-  // ---- transpose: w[32 b + 8 s + u] becomes, in lane group lg, row
-  // 32 b + 8 lg + u of pack chunk*64 + 16 s + lj.
-#pragma unroll
-  for (int b = 0; b < kSteps; ++b)
+  // ---- transpose of step b: w[32 b + 8 s + u] becomes, in lane group lg,
+  // row 32 b + 8 lg + u of pack chunk*64 + 16 s + lj. Then per pack set s:
+  // MFMAs over the wave's rows (acc[c][r] is row 4 lg + r of packed lane c
+  // of pack chunk*64 + 16 s + lj; columns of a pack in order take packed
+  // lane kAwqLaneOfCol[j] (AutoAWQ) or j (sequential)), scaled and written
+  // to this wave's LDS slot. s is a compile-time constant in each body
+  // (every register index must be static).
+  const bool seq = a.seq != 0;
+  auto transpose = [&](int b) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) tr4(w[32 * b + u], w[32 * b + 8 + u], w[32 * b + 16 + u], w[32 * b + 24 + u]);
-
-  // ---- per pack set s: MFMAs over the wave's rows, then scale and write the
-  // set's 8 x 128 partial sums to this wave's LDS slot. acc[c][r] is row
-  // 4 lg + r of packed lane c of pack chunk*64 + 16 s + lj; columns of a pack
-  // in order take packed lane kAwqLaneOfCol[j] (AutoAWQ) or j (sequential).
-  const bool seq = a.seq != 0;
-  // One body per pack set with s a compile-time constant: every register
-  // index below must be static (a runtime s turns w[...] into indexed moves).
-  auto pack_set = [&](auto s_const) {
+  };
+  auto mfmas = [&](auto s_const, int b, f32x4_t (&acc)[8]) {
     constexpr int s = decltype(s_const)::value;
-    f32x4_t acc[8];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    if (live) {
+    for (int c = 0; c < 8; ++c) {
+      const f16x2 fz = __builtin_bit_cast(f16x2, nib_f16x2(zq[s], zq[s], c));
+      f16x8_t bq;
 #pragma unroll
-      for (int b = 0; b < kSteps; ++b) {
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const f16x2 fz = __builtin_bit_cast(f16x2, nib_f16x2(zq[s], zq[s], c));
-          f16x8_t bq;
-#pragma unroll
-          for (int u = 0; u < 8; u += 2) {
-            const f16x2 d =
-                __builtin_bit_cast(f16x2, nib_f16x2(w[32 * b + 8 * s + u], w[32 * b + 8 * s + u + 1], c)) - fz;
-            bq[u] = d[0];
-            bq[u + 1] = d[1];
-          }
-          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b], bq, acc[c], 0, 0, 0);
-          if constexpr (kLo) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b], bq, acc[c], 0, 0, 0);
-        }
+      for (int u = 0; u < 8; u += 2) {
+        const f16x2 d = __builtin_bit_cast(f16x2, nib_f16x2(w[32 * b + 8 * s + u], w[32 * b + 8 * s + u + 1], c)) - fz;
+        bq[u] = d[0];
+        bq[u + 1] = d[1];
       }
+      acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[b], bq, acc[c], 0, 0, 0);
+      if constexpr (kLo) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[b], bq, acc[c], 0, 0, 0);
     }
+  };
+  // Scaled sums of pack set s; into this wave's slot (add: onto what it holds).
+  auto store_set = [&](auto s_const, const f32x4_t (&acc)[8], bool add) {
+    constexpr int s = decltype(s_const)::value;
     float sl[8], slp[8];
     scales_to_f32(sraw[s], a.st, sl);  // column order
     // Partial sums stay in packed-lane (slot) order; the scale of slot c is
     // that of its column (c in sequential order, kAwqColOfLane[c] in AutoAWQ).
 #pragma unroll
     for (int c = 0; c < 8; ++c) slp[c] = seq ? sl[c] : sl[awq_col_of_lane(c)];
-    float o[4][8];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * lg + r;
+      if (m < MV) {
+        float o[8];
 #pragma unroll
-      for (int c = 0; c < 8; ++c) o[r][c] = acc[c][r] * slp[c] * xdown[r];
-    auto store = [&](bool add) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = 4 * lg + r;
-        if (m < MV) {
-          float4* d4 = reinterpret_cast<float4*>(&red[slot][m][8 * (16 * s + lj)]);
-          float4 v0 = make_float4(o[r][0], o[r][1], o[r][2], o[r][3]);
-          float4 v1 = make_float4(o[r][4], o[r][5], o[r][6], o[r][7]);
-          if (add) {
-            const float4 p0 = d4[0], p1 = d4[1];
-            v0 = make_float4(v0.x + p0.x, v0.y + p0.y, v0.z + p0.z, v0.w + p0.w);
-            v1 = make_float4(v1.x + p1.x, v1.y + p1.y, v1.z + p1.z, v1.w + p1.w);
-          }
-          d4[0] = v0;
-          d4[1] = v1;
+        for (int c = 0; c < 8; ++c) o[c] = acc[c][r] * slp[c] * xdown[r];
+        float4* d4 = reinterpret_cast<float4*>(&red[slot][m][8 * (16 * s + lj)]);
+        float4 v0 = make_float4(o[0], o[1], o[2], o[3]);
+        float4 v1 = make_float4(o[4], o[5], o[6], o[7]);
+        if (add) {
+          const float4 p0 = d4[0], p1 = d4[1];
+          v0 = make_float4(v0.x + p0.x, v0.y + p0.y, v0.z + p0.z, v0.w + p0.w);
+          v1 = make_float4(v1.x + p1.x, v1.y + p1.y, v1.z + p1.z, v1.w + p1.w);
         }
+        d4[0] = v0;
+        d4[1] = v1;
       }
-    };
+    }
+  };
+  if (live) {
+#pragma unroll
+    for (int b = 0; b < kSteps; ++b) transpose(b);
+  }
+  // Per pack set, all steps' MFMAs, then the store. (Step by step instead,
+  // step 0's MFMAs starting while step 1's rows are in flight and each
+  // step's sums added into the slot, measured 5-13 % slower at 5..8 rows.)
+  // 16 rows: waves w and w + 4 share slot w (the upper waves store, the
+  // lower ones add after a barrier, per pack set).
+  auto pack_set = [&](auto s_const) {
+    f32x4_t acc[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) acc[c] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (live) {
+#pragma unroll
+      for (int b = 0; b < kSteps; ++b) mfmas(s_const, b, acc);
+    }
     if constexpr (kTwoRounds) {
-      if (wave >= kSlots) store(false);
+      if (wave >= kSlots) store_set(s_const, acc, false);
       __syncthreads();
-      if (wave < kSlots) store(true);
+      if (wave < kSlots) store_set(s_const, acc, true);
     } else {
-      store(false);
+      store_set(s_const, acc, false);
     }
   };
   pack_set(std::integral_constant<int, 0>{});
