@@ -25,11 +25,12 @@
 //    16-column MFMA tiles) for every 16-row tile, so each weight is
 //    dequantised once. Lane (lg = lane / 16, lj = lane % 16) reads the 8
 //    words of rows 8 lg .. 8 lg + 7 of pack 4 w + (lj & 3) from LDS and
-//    builds the B operand of tile t from packed lane c = 4 t + (lj >> 2)
-//    (64 columns: pack 2 w + (lj & 1), packed lane lj >> 1): one v_perm_b32 gathers
-//    byte c / 2 of two rows, one v_bitop3_b32 makes the f16 magic 1024 + q
+//    builds the B operands of tiles 0 and 1 from packed lanes 2 (lj >> 2)
+//    and 2 (lj >> 2) + 1, the two nibbles of one byte (64 columns: pack
+//    2 w + (lj & 1), packed lane lj >> 1): one v_perm_b32 gathers that byte
+//    of two rows, one v_bitop3_b32 per nibble makes the f16 magic 1024 + q
 //    (64 + q for the high nibble), then an exact v_pk_add_f16 of -(1024 + z)
-//    and one v_pk_mul_f16 by s: 2 VALU ops per weight. bf16 (no packed bf16
+//    and one v_pk_mul_f16 by s: 1.75 VALU ops per weight. bf16 (no packed bf16
 //    arithmetic on gfx950): after the same v_perm_b32, one v_and_b32 leaves
 //    q (or 16 q) in bytes 0 and 2, v_cvt_f32_ubyte0/2 convert them, one
 //    v_fma_f32 per weight forms q s' - z s = (q - z) s exactly (s' = s or
@@ -118,8 +119,11 @@ __device__ __forceinline__ void dma16(rsrc_t r, unsigned char* dst, uint32_t vof
 
 // Granule swizzle of an X row in LDS (64 bytes = four 16-byte granules):
 // granule g of row r sits in slot g ^ xswz(r), so the 16 rows one A-operand
-// read touches spread over all banks.
-__device__ __forceinline__ int xswz(int r) { return (r >> 2) & 3; }
+// read touches spread over all banks. Chosen among 22 candidates with a
+// probe kernel under SQ_LDS_BANK_CONFLICT: (r >> 1) & 3 reads conflict-free,
+// (r >> 2) & 3 cost 4 conflict cycles per ds_read_b128 (gfx950 serves a
+// 16-byte read in lane groups other than 16 consecutive lanes).
+__device__ __forceinline__ int xswz(int r) { return (r >> 1) & 3; }
 
 // ACT: the gate/up SiLU epilogue (store_out; AutoAWQ order only), a template
 // parameter so the plain kernel's code is untouched by it. BF: bf16
