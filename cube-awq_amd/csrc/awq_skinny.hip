@@ -602,7 +602,13 @@ void launch_mt(const GemmProblem& p) {
   // chunk for the last workgroup to sum (splits x M): beyond those the split-K
   // traffic and the serial reduction cost more than the extra workgroups gain
   // (measured on 4096..14336-deep, 4096..28672-wide problems, 32..128 rows).
-  int splits = (int)std::max<int64_t>(1, device_cus() / chunks);
+  // 64-column chunks of up to 64 rows fit two workgroups per CU (LDS and
+  // registers), and the second hides the first's latencies: twice the splits
+  // (4096 -> 4096 at M = 17 / 32 / 64: 13.6 / 13.9 / 15.4 -> 11.4 / 11.5 /
+  // 14.9 us; 14336 -> 4096 at M = 64: 36.2 -> 31.2; not at M = 128, where
+  // only one fits: 21.4 -> 25.8).
+  const int per_cu = (CW == 64 && MT <= 4) ? 2 : 1;
+  int splits = (int)std::max<int64_t>(1, per_cu * device_cus() / chunks);
   splits = std::min(splits, std::max(1, total_steps / 16));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (8 * p.rows)));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, 1024 / p.rows));
