@@ -146,7 +146,7 @@ constexpr int kCachePolicySC1 = 16;
 // release / acquire pair would add on gfx950 (one L2 per XCD):
 //  * Writer. Every partial is stored with an agent-scope atomic store or a
 //    buffer store with the same sc1 policy (kCachePolicySC1; 16-byte pieces
-//    where the partials are staged through LDS), which is written through
+//    in the skinny and 2..16-row decode kernels), which is written through
 //    its XCD's L2 to the device's point of
 //    coherence instead of staying dirty there; that writeback is what an
 //    agent-scope release adds, for plain stores only. Each wave then waits

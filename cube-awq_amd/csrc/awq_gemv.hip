@@ -420,106 +420,155 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t i, float (&v)[8])
 }
 
 // Sum a workgroup's slot-order partials over its LDS slots (fixed order),
-// publish them across K splits (agent-scope stores, completion wait, arrival
+// publish them across K splits (16-byte sc1 stores, completion wait, arrival
 // count; the last workgroup of the chunk sums the splits in order), add the
 // bias and store rows < rows of the chunk's 512 columns. red[w][m][8 p + c]
 // holds packed lane c of pack p (column c in sequential order,
-// kAwqColOfLane[c] in AutoAWQ order).
+// kAwqColOfLane[c] in AutoAWQ order). Each thread owns pieces of 4
+// consecutive slots of one row, kept in slot order until the final store
+// (the split partials too): 16-byte LDS reads without bank conflicts, and
+// 16-byte partial stores and loads (the vector memory path takes about 16
+// clocks per wave instruction whatever its width).
 template <int MV, int WAVES, int kSlots, bool ACT>
 __device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*red)[MV][512], int* s_last_p,
                                              int rows, bool seq) {
   constexpr int kChunkCols = 512;
+  constexpr int kQ = MV * kChunkCols / 4;  // 4-slot pieces of the chunk's outputs
+  constexpr int kTh = 64 * WAVES;
+  constexpr int kPer = (kQ + kTh - 1) / kTh;  // pieces per thread
+  typedef float f32x4_t __attribute__((ext_vector_type(4)));
   const int chunk = blockIdx.x;
   const int split = blockIdx.y;
+  const int tid = threadIdx.x;
   int& s_last = *s_last_p;
-  constexpr int kOut = MV * kChunkCols;
-  constexpr int kPer = (kOut + 64 * WAVES - 1) / (64 * WAVES);
-  float res[kPer];
+  const int col_base = chunk * kChunkCols;
+  // piece q: row q / 128, slots 4 (q % 128) .. + 3 of the chunk
+  f32x4_t res[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int o = threadIdx.x + i * 64 * WAVES;
-    float v = 0.f;
-    if (o < kOut) {
-      const int m = o / kChunkCols, c = o % kChunkCols;
-      // column c of its pack sits in slot c (sequential) or kAwqLaneOfCol[c]
-      // = (c >> 1) + 4 (c & 1) (AutoAWQ)
-      const int cs = (c & ~7) | (seq ? (c & 7) : ((c & 7) >> 1) + 4 * (c & 1));
+    const int q = tid + i * kTh;
+    f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    if (q < kQ) {
+      const int m = q / (kChunkCols / 4), s0 = 4 * (q % (kChunkCols / 4));
 #pragma unroll
-      for (int ww = 0; ww < kSlots; ++ww) v += red[ww][m][cs];
+      for (int ww = 0; ww < kSlots; ++ww) {
+        const f32x4_t r4 = *reinterpret_cast<const f32x4_t*>(&red[ww][m][s0]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += r4[e];
+      }
     }
     res[i] = v;
   }
 
-  const int col_base = chunk * kChunkCols;
   if (a.splits > 1) {
-    // Same handshake as the VALU path: agent-scope partial stores, completion
-    // wait, arrival count; the last workgroup sums the splits in order.
+    // Same handshake as the VALU path, with sc1 buffer stores and loads
+    // (split-K handshake, awq_common.h); the last workgroup sums the splits
+    // in order.
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * MV * a.N * 4));
+    const uint32_t sstride = (uint32_t)((int64_t)MV * a.N * 4);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int o = threadIdx.x + i * 64 * WAVES;
-      const int m = o / kChunkCols, c = o % kChunkCols;
-      if (o < kOut && m < rows && col_base + c < a.N)
-        __hip_atomic_store(&a.partial[((int64_t)split * MV + m) * a.N + col_base + c], res[i],
-                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int q = tid + i * kTh;
+      const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
+      if (q < kQ && m < rows && col_base + c0 < a.N) {
+        const float f0 = res[i][0], f1 = res[i][1], f2 = res[i][2], f3 = res[i][3];
+        const u32x4_t w4 = u32x4_t{__float_as_uint(f0), __float_as_uint(f1), __float_as_uint(f2), __float_as_uint(f3)};
+        __builtin_amdgcn_raw_buffer_store_b128(w4, pres, (uint32_t)(((int64_t)m * a.N + col_base + c0) * 4),
+                                               (uint32_t)split * sstride, kCachePolicySC1);
+      }
     }
     // Partials complete before the arrival (split-K handshake, awq_common.h).
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
       const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCounterStride], 1u,
                                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
     }
     __syncthreads();
     if (!s_last) return;
-    // Each thread's kPer outputs, kSB splits at a time: kPer * kSB loads in
-    // flight (one output after another would leave one CU latency-bound on
-    // splits x rows x 2 KB); every output still sums its splits in order.
-    constexpr int kSB = kPer >= 16 ? 4 : 8;
-    const int64_t stride = (int64_t)MV * a.N;
-    const float* src[kPer];
-    bool ok[kPer];
+    // Each thread's kPer pieces, kSB splits at a time: kPer * kSB loads in
+    // flight; every output still sums its splits in order.
+    constexpr int kSB = kPer >= 4 ? 4 : 8;
+    uint32_t off[kPer];
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
-      const int o = threadIdx.x + i * 64 * WAVES;
-      const int m = o / kChunkCols, c = o % kChunkCols;
-      ok[i] = o < kOut && m < rows && col_base + c < a.N;
+      const int q = min(tid + i * kTh, kQ - 1);
+      const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
       // Rows past M read row M-1's partials (cached, discarded): unconditional
       // loads keep the batch in flight.
-      src[i] = a.partial + (int64_t)min(m, rows - 1) * a.N + min(col_base + c, a.N - 1);
-      res[i] = 0.f;
+      off[i] = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
+      res[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
     for (int s0 = 0; s0 < a.splits; s0 += kSB) {
-      float t[kPer][kSB];
+      f32x4_t t[kPer][kSB];
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
 #pragma unroll
         for (int j = 0; j < kSB; ++j) {
           const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
-          t[i][j] = __hip_atomic_load(src[i] + sj * stride, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(pres, off[i], (uint32_t)sj * sstride,
+                                                                   kCachePolicySC1);
+          // through plain scalars (hipcc 7.2 misreads a bit cast of a vector element)
+          const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+          t[i][j] = f32x4_t{__uint_as_float(e0), __uint_as_float(e1), __uint_as_float(e2), __uint_as_float(e3)};
         }
 #pragma unroll
       for (int i = 0; i < kPer; ++i)
 #pragma unroll
-        for (int j = 0; j < kSB; ++j)
-          if (s0 + j < a.splits) res[i] += t[i][j];
+        for (int j = 0; j < kSB; ++j) {
+          const bool live = s0 + j < a.splits;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) res[i][e] += live ? t[i][j][e] : 0.f;
+        }
     }
-    if (threadIdx.x == 0)
+    if (tid == 0)
       __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
-  // and its xor-1 neighbour.
+  // Slots to columns. Sequential order: slot = column. AutoAWQ: the even
+  // lane of a pack holds slots 0..3 = columns 0, 2, 4, 6 and the odd lane
+  // slots 4..7 = columns 1, 3, 5, 7; one exchange leaves columns 0..3 in the
+  // even lane and 4..7 in the odd one. Then each lane stores 4 consecutive
+  // columns (a gate/up pair is elements 2 j, 2 j + 1).
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int o = threadIdx.x + i * 64 * WAVES;
-    const int m = o / kChunkCols, c = o % kChunkCols;
-    const int n = col_base + c;
-    float v = res[i];
-    if (a.bias && n < a.N) v += load_f32_any(a.bias, n, a.bt);
-    const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
-    if (o < kOut && m < rows && n < a.N) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
+    const int q = tid + i * kTh;
+    const int m = q / (kChunkCols / 4), n0 = col_base + 4 * (q % (kChunkCols / 4));
+    float v[4];
+    if (seq) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = res[i][e];
+    } else {
+      float x[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[e] = __shfl_xor(res[i][e], 1, 64);
+      const bool odd = (tid & 1) != 0;
+      v[0] = odd ? x[2] : res[i][0];
+      v[1] = odd ? res[i][2] : x[0];
+      v[2] = odd ? x[3] : res[i][1];
+      v[3] = odd ? res[i][3] : x[1];
+    }
+    if (q >= kQ || m >= rows || n0 >= a.N) continue;
+    if (a.bias) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += load_f32_any(a.bias, n0 + e, a.bt);
+    }
+    if (ACT) {
+      store_out(a.y, a.yt, 1, m, n0, a.N, v[0], v[1]);
+      store_out(a.y, a.yt, 1, m, n0 + 2, a.N, v[2], v[3]);
+    } else if (a.yt == AWQ_F32) {
+      typedef float f4_t __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<f4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n0) = f4_t{v[0], v[1], v[2], v[3]};
+    } else if (a.yt == AWQ_F16) {
+      typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+      *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n0) =
+          h4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) store_out(a.y, a.yt, 0, m, n0 + e, a.N, v[e], 0.f);
+    }
   }
 }
 
