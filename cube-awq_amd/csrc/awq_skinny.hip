@@ -545,9 +545,22 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
-        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
+        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread; plain
+        // outputs leave as one 16- or 8-byte store of the 4 columns.
+        if (ACT) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+          for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+        } else if (a.yt == AWQ_F32) {
+          *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n) =
+              f32x4_t{v[g][0], v[g][1], v[g][2], v[g][3]};
+        } else if (a.yt == AWQ_F16) {
+          typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n) =
+              h4_t{(_Float16)v[g][0], (_Float16)v[g][1], (_Float16)v[g][2], (_Float16)v[g][3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, 0, m, n + q, a.N, v[g][q], 0.f);
+        }
       }
     }
     if (tid == 0)
