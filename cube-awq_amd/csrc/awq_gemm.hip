@@ -1020,18 +1020,45 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     // re-reads all splits' partials (agent-scope loads, split order, in a
     // coalesced row-major walk of the tile), adds the bias and writes y, and
     // re-arms the counter.
-    float* part = a.partial + (int64_t)split * a.M * a.N;
+    // The partial tile passes through the (idle) LDS in row passes and leaves
+    // as 16-byte pieces of whole rows with the sc1 policy: a wave store
+    // instruction moves 1 KB instead of 256 scattered bytes (the vector
+    // memory path takes about 16 clocks per instruction whatever its width).
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
+    const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
+    {
+      constexpr int pitch = BN * 4 + 16;  // bytes per staged row (bank spread)
+      constexpr int fit = (int)(C::kSmem / pitch) & ~(MS - 1);
+      constexpr int rows_pass = fit < BM ? fit : BM;
+      constexpr int gran = BN / 4;  // 16-byte pieces per tile row
+      static_assert(rows_pass >= MS, "staged rows");
+      // LDS-direct prefetches of clamped tail stages may still be landing.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      for (int p0 = 0; p0 < BM; p0 += rows_pass) {
+        __syncthreads();
 #pragma unroll
-    for (int j = 0; j < C::kJ; ++j) {
-      const int n = out_col(j);
+        for (int j = 0; j < C::kJ; ++j) {
+          const int lc = out_col(j) - n0;
 #pragma unroll
-      for (int i = 0; i < C::kI; ++i) {
+          for (int i = 0; i < C::kI; ++i) {
 #pragma unroll
-        for (int r = 0; r < kAccN; ++r) {
-          const int m = out_row(i, r);
+            for (int r = 0; r < kAccN; ++r) {
+              const int lr = out_row(i, r) - m0 - p0;
+              if (rows_pass < BM && (lr < 0 || lr >= rows_pass)) continue;
+              *reinterpret_cast<float*>(smem_raw + lr * pitch + lc * 4) = acc[i][j][r];
+            }
+          }
+        }
+        __syncthreads();
+        const int rows = min(rows_pass, BM - p0);
+        for (int g = tid; g < rows * gran; g += C::kThreads) {
+          const int row = g / gran, gc = g % gran;
+          const int m = m0 + p0 + row;
+          const int n = n0 + gc * 4;  // N % 32 == 0: a piece is all in or all out
           if (m < a.M && n < a.N)
-            __hip_atomic_store(&part[(int64_t)m * a.N + n], acc[i][j][r], __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_raw_buffer_store_b128(*reinterpret_cast<const u32x4*>(smem_raw + row * pitch + gc * 16),
+                                                   pres, (uint32_t)(((int64_t)m * a.N + n) * 4),
+                                                   (uint32_t)split * sstride, kCachePolicySC1);
         }
       }
     }
@@ -1055,8 +1082,6 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     // splits x tile partials: ~30 us for a 128 x 128 tile and 8 splits.)
     // Every slot is loaded (indices clamped into the workspace) and only the
     // valid ones are added and stored, so nothing read is ever undefined.
-    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
-    const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
     constexpr int kG = 4;
     constexpr int kStep4 = C::kThreads * 4;
     for (int e0 = tid * 4; e0 < BM * BN; e0 += kG * kStep4) {
@@ -1105,9 +1130,23 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
-        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread.
+        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread; plain
+        // outputs leave as one 16- or 8-byte store of the 4 columns.
+        if (ACT) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+          for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+        } else if (a.yt == AWQ_F32) {
+          *reinterpret_cast<u32x4*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n) =
+              u32x4{__float_as_uint(v[g][0]), __float_as_uint(v[g][1]), __float_as_uint(v[g][2]),
+                    __float_as_uint(v[g][3])};
+        } else if (a.yt == AWQ_F16) {
+          typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+          *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n) =
+              h4_t{(_Float16)v[g][0], (_Float16)v[g][1], (_Float16)v[g][2], (_Float16)v[g][3]};
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, 0, m, n + q, a.N, v[g][q], 0.f);
+        }
       }
     }
     if (tid == 0)
