@@ -107,6 +107,25 @@ __device__ __forceinline__ void store_out(void* y, int32_t yt, int32_t act, int6
   else if ((n & 1) == 0) store_f32_any(y, m * (N >> 1) + (n >> 1), yt, silu_mul(v, partner));
 }
 
+// The activation outputs of 4 consecutive GEMM columns n .. n + 3 (n % 4 ==
+// 0: gate/up pairs (n, n + 1) and (n + 2, n + 3)), two consecutive outputs
+// of row m, written as one 8-byte (f32) or 4-byte (f16, bf16) store.
+__device__ __forceinline__ void store_act_quad(void* y, int32_t yt, int64_t m, int64_t n, int64_t N, float g0,
+                                               float u0, float g1, float u1) {
+  const int64_t i = m * (N >> 1) + (n >> 1);
+  const float o0 = silu_mul(g0, u0), o1 = silu_mul(g1, u1);
+  if (yt == AWQ_F32) {
+    typedef float f2_t __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<f2_t*>(static_cast<float*>(y) + i) = f2_t{o0, o1};
+  } else if (yt == AWQ_F16) {
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<h2_t*>(static_cast<f16_t*>(y) + i) = h2_t{(_Float16)o0, (_Float16)o1};
+  } else {
+    store_f32_any(y, i, yt, o0);
+    store_f32_any(y, i + 1, yt, o1);
+  }
+}
+
 // Packed lane L of two words as f16x2 magic numbers: the byte holding lane L
 // of w0 and of w1 goes to the two halves (v_perm_b32), then one v_bitop3
 // keeps the nibble and ORs in the exponent: low nibble (even L) -> 0x6400 | q

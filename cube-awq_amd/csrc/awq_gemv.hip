@@ -556,8 +556,7 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*re
       for (int e = 0; e < 4; ++e) v[e] += load_f32_any(a.bias, n0 + e, a.bt);
     }
     if (ACT) {
-      store_out(a.y, a.yt, 1, m, n0, a.N, v[0], v[1]);
-      store_out(a.y, a.yt, 1, m, n0 + 2, a.N, v[2], v[3]);
+      store_act_quad(a.y, a.yt, m, n0, a.N, v[0], v[1], v[2], v[3]);
     } else if (a.yt == AWQ_F32) {
       typedef float f4_t __attribute__((ext_vector_type(4)));
       *reinterpret_cast<f4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n0) = f4_t{v[0], v[1], v[2], v[3]};

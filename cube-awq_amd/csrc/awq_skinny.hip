@@ -548,8 +548,7 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
         // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread; plain
         // outputs leave as one 16- or 8-byte store of the 4 columns.
         if (ACT) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, ACT, m, n + q, a.N, v[g][q], v[g][q ^ 1]);
+          store_act_quad(a.y, a.yt, m, n, a.N, v[g][0], v[g][1], v[g][2], v[g][3]);
         } else if (a.yt == AWQ_F32) {
           *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n) =
               f32x4_t{v[g][0], v[g][1], v[g][2], v[g][3]};
