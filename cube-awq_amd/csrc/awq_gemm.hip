@@ -1205,24 +1205,54 @@ __global__ __launch_bounds__(64 * WGM * WGN, 1) void gemm_big_kernel(GemmArgs a)
     else staged(std::integral_constant<int, 2>{});
     return;
   }
-  // Column lane % 32 (or % 16): a gate/up pair is this lane and its xor-1
-  // neighbour (N is even, so both are in range or neither).
+  // SiLU(gate) * up: column lane % 32 (or % 16) and its xor-1 neighbour are
+  // a gate/up pair; the even lane's output (column n / 2 of the half-width
+  // Y) goes into the staged half-width tile (it fits the LDS in one pass),
+  // which leaves as 16-byte pieces of whole rows.
+  auto staged_act = [&](auto es_c) {
+    constexpr int es = decltype(es_c)::value;
+    constexpr int kHW = BN / 2;
+    constexpr int pitch = kHW * es + 16;
+    constexpr int gran = kHW * es / 16;  // 16-byte pieces per half-width row
+    static_assert((size_t)BM * pitch <= C::kSmem && (kHW * es) % 16 == 0, "staged half-width tile");
+    char* yb = static_cast<char*>(a.y);
+    const int64_t hn = a.N >> 1;
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < C::kJ; ++j) {
-    const int n = out_col(j);
-    if (n >= a.N) continue;
-    const float bias = a.bias ? load_f32_any(a.bias, n, a.bt) : 0.f;
+    for (int j = 0; j < C::kJ; ++j) {
+      const int n = out_col(j);
+      const float bias = (a.bias && n < a.N) ? load_f32_any(a.bias, n, a.bt) : 0.f;
+      const int lc = (n - n0) >> 1;
+      const bool even = (n & 1) == 0;
 #pragma unroll
-    for (int i = 0; i < C::kI; ++i) {
+      for (int i = 0; i < C::kI; ++i) {
 #pragma unroll
-      for (int r = 0; r < kAccN; ++r) {
-        const int m = out_row(i, r);
-        const float v = acc[i][j][r] + bias;
-        const float pv = ACT ? __shfl_xor(v, 1, 64) : 0.f;
-        if (m < a.M) store_out(a.y, a.yt, ACT, m, n, a.N, v, pv);
+        for (int r = 0; r < kAccN; ++r) {
+          const float v = acc[i][j][r] + bias;
+          const float pv = __shfl_xor(v, 1, 64);
+          if (even) {
+            const float o = silu_mul(v, pv);
+            unsigned char* d = smem_raw + (out_row(i, r) - m0) * pitch + lc * es;
+            if constexpr (es == 4) *reinterpret_cast<float*>(d) = o;
+            else if (a.yt == AWQ_BF16) *reinterpret_cast<bf16_t*>(d) = from_f32<bf16_t>(o);
+            else *reinterpret_cast<f16_t*>(d) = from_f32<f16_t>(o);
+          }
+        }
       }
     }
-  }
+    __syncthreads();
+    for (int g = tid; g < BM * gran; g += C::kThreads) {
+      const int row = g / gran, gc = g % gran;
+      const int m = m0 + row;
+      const int64_t n2 = (n0 >> 1) + gc * 16 / es;  // N / 2 % 16 == 0: a piece is all in or all out
+      const u32x4 v = *reinterpret_cast<const u32x4*>(smem_raw + row * pitch + gc * 16);
+      if (m < a.M && n2 < hn) *reinterpret_cast<u32x4*>(yb + ((int64_t)m * hn + n2) * es) = v;
+    }
+  };
+  // LDS-direct prefetches of clamped tail stages may still be landing.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (a.yt == AWQ_F32) staged_act(std::integral_constant<int, 4>{});
+  else staged_act(std::integral_constant<int, 2>{});
 }
 
 // Prepass of MODE_F32S: one workgroup per row of x [M, K] f32 (K % 4 == 0).
