@@ -1463,12 +1463,24 @@ void launch_mode(const GemmProblem& p) {
         // to the last workgroup's sum of 8 partial tiles). Measured at
         // M = 129..768, K 4096..28672, N 1024..14336: e.g. 14336 -> 4096 at
         // M = 256 175 -> 62 us, 28672 -> 8192 at M = 256 218 -> 180 us.
+        // On equal time the wider tile wins if it needs no more K splits; if
+        // it needs more, the narrower one wins unless it needs splits too
+        // and the wider one keeps >= 24 stages per split (the extra split
+        // costs the last workgroup one more partial tile to sum). Measured:
+        // 1024 x 8192 -> 1024 42.1 -> 39.3 us, 1024 x 4096 -> 4096 59.5 ->
+        // 56.9, 512 x 4096 -> 4096 42.1 -> 41.1, 256 x 4096 -> 14336 59.4 ->
+        // 57.1, 768 x 4096 -> 4096 54.2 -> 52.2; 256 x 14336 -> 4096 (28
+        // stages per split) and 384 x 4096 -> 14336 (one split either way,
+        // 72.5 against 100.5) keep the wider tile.
         splits = pow2_splits(t);
         const int64_t t3 = tiles(128, 256);
         const int s3 = pow2_splits(t3);
         const int64_t cus = device_cus();
         const int64_t waves4 = (t * splits + cus - 1) / cus, waves3 = (t3 * s3 + cus - 1) / cus;
-        if (2 * waves3 * splits <= waves4 * s3 && (s3 <= 4 || stages / s3 >= 16)) {
+        const bool wider = 2 * waves3 * splits < waves4 * s3 ||
+                           (2 * waves3 * splits == waves4 * s3 &&
+                            (s3 <= splits || (splits > 1 && stages / s3 >= 24)));
+        if (wider && (s3 <= 4 || stages / s3 >= 16)) {
           cfg = 12;
           splits = s3;
         }
