@@ -32,7 +32,10 @@ matrix-core work after the memory-bound phases) and a device synchronise on
 both sides. The M=2048 prefill also replays about 200 untimed calls right
 before the timed ones with no synchronisation in between: after the idle gap
 of the synchronise the clock ramps again (measured 238 us per call without
-them, 222 us with them, on one box). `roofline.achieved` = algorithmic bytes
+them, 222 us with them, on one box). The rows of `decode_rows`,
+`prefill_rows`, the fp32 prefill, the gate/up SiLU pair and `--sweep` replay
+about 20 ms of untimed calls the same way before timing (mid-size prefill
+points measured 2-12 % slow without). `roofline.achieved` = algorithmic bytes
 (flops) per launch / average launch duration from those events.
 Beside each graph-replay figure, `eager_us_per_call` times the reference
 bench's own protocol (benches/awq_kernel_gemm.rs:318-340): wall clock around
@@ -138,7 +141,7 @@ def sweep(dev, np, torch, synth, _lib, call_gemm, graph_time, points=None, steps
                 if steps_override:
                     steps = steps_override
                 warm = 5 if flops < 5e11 else 100  # clock ramp on long matrix-core runs
-                ms, _, _ = graph_time(launch, min(100, steps), warm, steps)
+                ms, _, _ = graph_time(launch, min(100, steps), warm, steps, warm_replays=-1)
                 nbytes = w_bytes + M * K * xs + M * N * xs
                 gbs = nbytes / (ms * 1e-3) / 1e9
                 tflops = flops / (ms * 1e-3) / 1e12
@@ -192,7 +195,8 @@ def main():
         `warm_replays` untimed replays run right before the timed ones, with
         no synchronisation in between, so the timed calls start on a GPU that
         is already busy (matrix-core-heavy calls run at a lower clock for
-        tens of milliseconds after an idle gap)."""
+        tens of milliseconds after an idle gap); -1: as many as make about
+        20 ms, from one timed replay."""
         per_graph = max(1, min(per_graph, steps))
         torch.cuda.synchronize()
         with torch.cuda.stream(run_stream):
@@ -215,6 +219,13 @@ def main():
         with torch.cuda.stream(run_stream):
             graphs[0][0].replay()  # untimed: first replay uploads the graph
             torch.cuda.synchronize()
+            if warm_replays < 0:
+                w0, w1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                w0.record(run_stream)
+                graphs[0][0].replay()
+                w1.record(run_stream)
+                w1.synchronize()
+                warm_replays = min(200, math.ceil(20.0 / max(w0.elapsed_time(w1), 1e-3)))
             for _ in range(warm_replays):
                 graphs[0][0].replay()
             t0 = time.perf_counter()
@@ -295,7 +306,7 @@ def main():
                     w = ws[i % copies]
                     call_gemm(xr, _lib.AWQ_F32, w[0], w[1], w[2], _lib.AWQ_F16, yr, _lib.AWQ_F32, mr, K, N, G)
 
-                rms, _, _ = graph_time(dec_r, 100, 50, 2000)
+                rms, _, _ = graph_time(dec_r, 100, 50, 2000, warm_replays=-1)
                 out["decode_rows"][mr] = dict(us=rms * 1e3, gbs=r_bytes / (rms * 1e-3) / 1e9)
 
             # The CPU-baseline configuration: 4096 -> 4096, g128, f32 x, f32
@@ -386,8 +397,8 @@ def main():
                     call_gemm(xr, xt, w[6], w[7], w[8], _lib.AWQ_F16, yu, xt, mr, K, N, G)
                     torch.mul(torch.nn.functional.silu(yg), yu, out=ys)
 
-                fms, _, _ = graph_time(fused, 50, 20, 500)
-                ums, _, _ = graph_time(unfused, 50, 20, 500)
+                fms, _, _ = graph_time(fused, 50, 20, 500, warm_replays=-1)
+                ums, _, _ = graph_time(unfused, 50, 20, 500, warm_replays=-1)
                 out["gate_up_silu"][mr] = dict(fused_us=fms * 1e3, unfused_us=ums * 1e3)
             del gw
 
@@ -427,7 +438,7 @@ def main():
                     w = pw[i % pcopies]
                     call_gemm(xr, _lib.AWQ_F16, w[0], w[1], w[2], _lib.AWQ_F16, yr, _lib.AWQ_F16, mr, K, N, G)
 
-                rms, _, _ = graph_time(pre_r, 20, 10, 200)
+                rms, _, _ = graph_time(pre_r, 20, 10, 200, warm_replays=-1)
                 out["prefill_rows"][mr] = dict(us=rms * 1e3, tflops=2.0 * mr * N * K / (rms * 1e-3) / 1e12)
             # fp32 activations (the reference's own float type) at prefill
             # sizes: x split into f16 hi + lo on the matrix cores, f32 output.
@@ -440,7 +451,7 @@ def main():
                     w = pw[i % pcopies]
                     call_gemm(xf, _lib.AWQ_F32, w[0], w[1], w[2], _lib.AWQ_F16, yf, _lib.AWQ_F32, mr, K, N, G)
 
-                rms, _, _ = graph_time(pre_f, pcopies, 20, 50)
+                rms, _, _ = graph_time(pre_f, pcopies, 20, 50, warm_replays=-1)
                 out["prefill_f32_rows"][mr] = dict(us=rms * 1e3, tflops=2.0 * mr * N * K / (rms * 1e-3) / 1e12)
                 del xf, yf
             # Context, not a roofline: the library dense fp16 GEMM (torch ->
