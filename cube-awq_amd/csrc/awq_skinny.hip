@@ -621,8 +621,12 @@ void launch_mt(const GemmProblem& p) {
   // only one fits: 21.4 -> 25.8).
   const int per_cu = (CW == 64 && MT <= 4) ? 2 : 1;
   int splits = (int)std::max<int64_t>(1, per_cu * device_cus() / chunks);
-  splits = std::min(splits, std::max(1, total_steps / 16));
-  splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / (8 * p.rows)));
+  // A grid that those limits would leave under one workgroup per CU (few
+  // chunks) takes runs down to 8 steps and partials up to twice the packed
+  // weights instead (4096 -> 1024 at M = 64: 8 -> 16 splits, 10.6 -> 10.0 us).
+  const bool few = (int64_t)chunks * std::min(splits, std::max(1, total_steps / 16)) < device_cus();
+  splits = std::min(splits, std::max(1, total_steps / (few ? 8 : 16)));
+  splits = std::min<int64_t>(splits, std::max<int64_t>(1, p.K / ((few ? 4 : 8) * p.rows)));
   splits = std::min<int64_t>(splits, std::max<int64_t>(1, 1024 / p.rows));
   if (int v = tuning(kTuneSkinnySplits, 0); v >= 1) splits = std::min(v, total_steps);
   int sps = (total_steps + splits - 1) / splits;
@@ -696,7 +700,13 @@ void launch_rows(const GemmProblem& p) {
   // 256 columns over 8 waves: on 4 waves of 64 columns (half the X reads
   // from LDS, one wave per SIMD) 4096 -> 14336 at M = 64 measured 33.9
   // against 26.1 us, the LDS and dependency latencies no longer hidden.
-  if (cols == 256 || (cols != 64 && p.N >= 6144)) return launch_rows_cw<BF, 256, 8>(p);
+  // Very deep K also favours the wide chunks (their K splits keep long
+  // runs): 14336 -> 4096 at M = 17 / 32 / 64 22.5 / 22.8 / 30.8 -> 20.7 /
+  // 21.4 / 29.9 us, 28672 -> 4096 at M = 64 53.0 -> 41.7; not at 33..48 rows
+  // (three row tiles: 26.8 -> 28.6) or at K = 8192 / 11008 (the 64-column
+  // chunks stay 5-19 % ahead).
+  const bool deep = p.K >= 14336 && (p.rows <= 32 || p.rows > 48);
+  if (cols == 256 || (cols != 64 && (p.N >= 6144 || deep))) return launch_rows_cw<BF, 256, 8>(p);
   return launch_rows_cw<BF, 64, 4>(p);
 }
 
