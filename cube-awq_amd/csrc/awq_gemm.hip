@@ -1464,14 +1464,15 @@ void launch_mode(const GemmProblem& p) {
         // M = 129..768, K 4096..28672, N 1024..14336: e.g. 14336 -> 4096 at
         // M = 256 175 -> 62 us, 28672 -> 8192 at M = 256 218 -> 180 us.
         // On equal time the wider tile wins if it needs no more K splits; if
-        // it needs more, the narrower one wins unless it needs splits too
-        // and the wider one keeps >= 24 stages per split (the extra split
-        // costs the last workgroup one more partial tile to sum). Measured:
+        // it needs more, only with enough stages per split to amortise the
+        // extra partial tile its last workgroup sums: >= 24, or >= 48 when
+        // the narrower tile needs no split at all. Measured (narrower wins):
         // 1024 x 8192 -> 1024 42.1 -> 39.3 us, 1024 x 4096 -> 4096 59.5 ->
         // 56.9, 512 x 4096 -> 4096 42.1 -> 41.1, 256 x 4096 -> 14336 59.4 ->
-        // 57.1, 768 x 4096 -> 4096 54.2 -> 52.2; 256 x 14336 -> 4096 (28
-        // stages per split) and 384 x 4096 -> 14336 (one split either way,
-        // 72.5 against 100.5) keep the wider tile.
+        // 57.1, 768 x 4096 -> 4096 54.2 -> 52.2; (wider wins) 256 x 14336 ->
+        // 4096 (28 stages per split) 54.2 against 56.4, 512 x 28672 -> 8192
+        // (224) 278 against 346, 384 x 4096 -> 14336 (one split either way)
+        // 72.5 against 100.5.
         splits = pow2_splits(t);
         const int64_t t3 = tiles(128, 256);
         const int s3 = pow2_splits(t3);
@@ -1479,7 +1480,7 @@ void launch_mode(const GemmProblem& p) {
         const int64_t waves4 = (t * splits + cus - 1) / cus, waves3 = (t3 * s3 + cus - 1) / cus;
         const bool wider = 2 * waves3 * splits < waves4 * s3 ||
                            (2 * waves3 * splits == waves4 * s3 &&
-                            (s3 <= splits || (splits > 1 && stages / s3 >= 24)));
+                            (s3 <= splits || stages / s3 >= (splits > 1 ? 24 : 48)));
         if (wider && (s3 <= 4 || stages / s3 >= 16)) {
           cfg = 12;
           splits = s3;
