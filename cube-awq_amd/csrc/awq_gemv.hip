@@ -33,8 +33,10 @@
 //  * The waves of a workgroup (stacked along K) are summed through LDS in a
 //    fixed order. When K needs more than one workgroup per column chunk
 //    (grid.y = splits), each writes its partial and the last to arrive sums
-//    them in split order (handshake below); arrival counters sit on separate
-//    256-byte lines so chunks do not serialise on one line.
+//    them in a fixed order (split order; with more than 8 splits, contiguous
+//    split ranges per thread group, then the groups in order:
+//    grouped_split_sum); arrival counters sit on separate 256-byte lines so
+//    chunks do not serialise on one line.
 //
 // Algorithmic HBM bytes per call: K*N/2 (qweight) + (K/g)*(N/8)*4 (qzeros) +
 // (K/g)*N*sizeof(scale) + M*K*sizeof(x) + M*N*sizeof(y).
@@ -69,6 +71,7 @@ __device__ __forceinline__ float load_x(const void* x, int64_t i) {
 }
 
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 // Raw bytes of the 8 scales of one packed word: 32 bytes for f32 scales, 16
 // for f16/bf16 (the second load then repeats the first). Issued without any
@@ -143,8 +146,88 @@ __device__ __forceinline__ void fma_word(float (&acc)[8], float x, const h2_t (&
 
 constexpr int kCounterStride = 64;  // u32 words between arrival counters (256 B)
 
-// ACT (both decode kernels): the gate/up SiLU epilogue (store_out), a template
-// parameter so the plain kernels' code is untouched by it.
+// Split-K sums with more splits than a single batch of loads: the last
+// workgroup of a chunk sums the partials of its kQ 4-column pieces with kG
+// thread groups (threads kG * kQ of the workgroup; piece q = tid % kQ, group
+// h = tid / kQ, uniform per wave since kQ is a multiple of 64). Group h sums
+// splits [h per, (h + 1) per) in order with all of its 16-byte loads in
+// flight; the kG group sums meet in lds (kG * kQ 16-byte entries) and are
+// added in group order. Returns the piece's total in threads tid < kQ; every
+// thread of the workgroup calls it (it holds a barrier). The partials are
+// laid out [split][MV][N] f32, columns in order.
+template <int MV, int kQ, int kG>
+__device__ __forceinline__ f32x4_t grouped_split_sum(const GemvArgs& a, f32x4_t* lds, int rows, int col_base) {
+  const int tid = threadIdx.x;
+  const int q = tid % kQ, h = tid / kQ;
+  const int m = q / 128, c0 = 4 * (q % 128);
+  const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * MV * a.N * 4));
+  const uint32_t sstride = (uint32_t)((int64_t)MV * a.N * 4);
+  const uint32_t off = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
+  const int per = (a.splits + kG - 1) / kG;
+  const int sb = min(h * per, a.splits), se = min(sb + per, a.splits);
+  f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto run = [&](auto nb) {
+    constexpr int NB = decltype(nb)::value;
+    for (int s0 = sb; s0 < se; s0 += NB) {
+      f32x4_t t[NB];
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int sj = min(s0 + j, se - 1);  // clamped: stays in the group's range
+        const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(pres, off, (uint32_t)sj * sstride, kCachePolicySC1);
+        // through plain scalars (hipcc 7.2 misreads a bit cast of a vector element)
+        const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+        t[j] = f32x4_t{__uint_as_float(e0), __uint_as_float(e1), __uint_as_float(e2), __uint_as_float(e3)};
+      }
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const bool live = s0 + j < se;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += live ? t[j][e] : 0.f;
+      }
+    }
+  };
+  if (per <= 2) run(std::integral_constant<int, 2>{});
+  else run(std::integral_constant<int, 4>{});
+  lds[tid] = v;
+  __syncthreads();
+  f32x4_t r = v;
+  if (tid < kQ) {
+    r = lds[tid];
+#pragma unroll
+    for (int g = 1; g < kG; ++g) {
+      const f32x4_t r4 = lds[g * kQ + tid];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) r[e] += r4[e];
+    }
+  }
+  return r;
+}
+
+// Bias, then the store of 4 consecutive columns n0 .. n0 + 3 of row m (one
+// vector store for f32 and f16 outputs; with ACT the 2 SiLU outputs of the
+// gate/up pairs (n0, n0 + 1), (n0 + 2, n0 + 3)).
+template <bool ACT>
+__device__ __forceinline__ void store_cols4(const GemvArgs& a, int64_t m, int64_t n0, float (&v)[4]) {
+  if (a.bias) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += load_f32_any(a.bias, n0 + e, a.bt);
+  }
+  if (ACT) {
+    store_act_quad(a.y, a.yt, m, n0, a.N, v[0], v[1], v[2], v[3]);
+  } else if (a.yt == AWQ_F32) {
+    *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.y) + m * a.N + n0) = f32x4_t{v[0], v[1], v[2], v[3]};
+  } else if (a.yt == AWQ_F16) {
+    typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+    *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + m * a.N + n0) =
+        h4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) store_out(a.y, a.yt, 0, m, n0 + e, a.N, v[e], 0.f);
+  }
+}
+
+// ACT (all decode kernels): the gate/up SiLU epilogue, a template parameter
+// so the plain kernels' code is untouched by it.
 template <int XT, int MT, int WAVES, int RPW, bool ACT>
 __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
   constexpr int kChunkCols = 512;  // 64 lanes x 8 columns
@@ -295,7 +378,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     // partials written with agent-scope (write-through, sc1) stores, the wave
     // waits for their completion (vmcnt 0), and only then the workgroup's
     // arrival is counted. The last workgroup to arrive for this chunk reads
-    // all partials with agent-scope (sc1) loads, sums them in split order,
+    // all partials with agent-scope (sc1) loads, sums them in a fixed order,
     // and re-arms the counter for the next call.
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -315,6 +398,27 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    // More than 8 splits (deep K): 4-column pieces, the splits shared by
+    // thread groups (grouped_split_sum), one round of loads instead of one
+    // per 8 splits (14336 -> 4096 at one row: 28 splits).
+    constexpr int kQ = MT * kChunkCols / 4;
+    if constexpr (kQ < 64 * WAVES) {
+      if (a.splits > 8) {
+        // The slots are free: every thread read its slots before the arrival barrier.
+        const f32x4_t r = grouped_split_sum<MT, kQ, 64 * WAVES / kQ>(
+            a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base);
+        const int q = threadIdx.x;
+        const int m = q / (kChunkCols / 4), n0 = col_base + 4 * (q % (kChunkCols / 4));
+        if (q < kQ && m < rows && n0 < a.N) {
+          float v[4] = {r[0], r[1], r[2], r[3]};
+          store_cols4<ACT>(a, m, n0, v);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int o = threadIdx.x + i * 64 * WAVES;
@@ -337,9 +441,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
         res[i] = v;
       }
     }
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
@@ -386,7 +487,6 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
 // through the workspace exactly as in the VALU path.
 // ---------------------------------------------------------------------------
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef h2_t f16x2;
 
 __device__ __forceinline__ void tr4(uint32_t& r0, uint32_t& r1, uint32_t& r2, uint32_t& r3) {
@@ -421,8 +521,10 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t i, float (&v)[8])
 
 // Sum a workgroup's slot-order partials over its LDS slots (fixed order),
 // publish them across K splits (16-byte sc1 stores, completion wait, arrival
-// count; the last workgroup of the chunk sums the splits in order), add the
-// bias and store rows < rows of the chunk's 512 columns. red[w][m][8 p + c]
+// count; the last workgroup of the chunk sums the splits in a fixed order:
+// split order, or, with more threads than pieces, contiguous split ranges
+// per thread group, then the groups in order), add the bias and store rows <
+// rows of the chunk's 512 columns. red[w][m][8 p + c]
 // holds packed lane c of pack p (column c in sequential order,
 // kAwqColOfLane[c] in AutoAWQ order). Each thread owns pieces of 4
 // consecutive slots of one row, kept in slot order until the final store
@@ -430,13 +532,16 @@ __device__ __forceinline__ void load_x8(const void* x, int64_t i, float (&v)[8])
 // 16-byte partial stores and loads (the vector memory path takes about 16
 // clocks per wave instruction whatever its width).
 template <int MV, int WAVES, int kSlots, bool ACT>
-__device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*red)[MV][512], int* s_last_p,
-                                             int rows, bool seq) {
+__device__ __forceinline__ void finish_chunk(const GemvArgs& a, float (*red)[MV][512], int* s_last_p, int rows,
+                                             bool seq) {
   constexpr int kChunkCols = 512;
   constexpr int kQ = MV * kChunkCols / 4;  // 4-slot pieces of the chunk's outputs
   constexpr int kTh = 64 * WAVES;
   constexpr int kPer = (kQ + kTh - 1) / kTh;  // pieces per thread
-  typedef float f32x4_t __attribute__((ext_vector_type(4)));
+  // Thread groups that share the last workgroup's sum over the K splits when
+  // the workgroup has more threads than pieces (grouped_split_sum).
+  constexpr int kG = kQ >= kTh ? 1 : kTh / kQ;
+  static_assert(kG == 1 || kSlots * kQ >= kTh, "LDS slots too small for the grouped split sum");
   const int chunk = blockIdx.x;
   const int split = blockIdx.y;
   const int tid = threadIdx.x;
@@ -487,44 +592,54 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*re
     }
     __syncthreads();
     if (!s_last) return;
-    // Each thread's kPer pieces, kSB splits at a time: kPer * kSB loads in
-    // flight; every output still sums its splits in order.
-    constexpr int kSB = kPer >= 4 ? 4 : 8;
-    uint32_t off[kPer];
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int q = min(tid + i * kTh, kQ - 1);
-      const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
-      // Rows past M read row M-1's partials (cached, discarded): unconditional
-      // loads keep the batch in flight.
-      off[i] = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
-      res[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
-    for (int s0 = 0; s0 < a.splits; s0 += kSB) {
-      f32x4_t t[kPer][kSB];
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-#pragma unroll
-        for (int j = 0; j < kSB; ++j) {
-          const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
-          const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(pres, off[i], (uint32_t)sj * sstride,
-                                                                   kCachePolicySC1);
-          // through plain scalars (hipcc 7.2 misreads a bit cast of a vector element)
-          const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
-          t[i][j] = f32x4_t{__uint_as_float(e0), __uint_as_float(e1), __uint_as_float(e2), __uint_as_float(e3)};
-        }
-#pragma unroll
-      for (int i = 0; i < kPer; ++i)
-#pragma unroll
-        for (int j = 0; j < kSB; ++j) {
-          const bool live = s0 + j < a.splits;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) res[i][e] += live ? t[i][j][e] : 0.f;
-        }
-    }
     if (tid == 0)
       __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+    bool grouped = false;
+    if constexpr (kG > 1) grouped = a.splits > 8;
+    if (grouped) {
+      // More threads than pieces and more than 8 splits: one round of loads
+      // shared by kG thread groups (the slots are free: every thread read its
+      // slots before the arrival barrier).
+      if constexpr (kG > 1)
+        res[0] = grouped_split_sum<MV, kQ, kG>(a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base);
+    } else {
+      // Each thread's kPer pieces, kSB splits at a time: kPer * kSB loads in
+      // flight; every output still sums its splits in order.
+      constexpr int kSB = kPer >= 4 ? 4 : 8;
+      uint32_t off[kPer];
+#pragma unroll
+      for (int i = 0; i < kPer; ++i) {
+        const int q = min(tid + i * kTh, kQ - 1);
+        const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
+        // Rows past M read row M-1's partials (cached, discarded): unconditional
+        // loads keep the batch in flight.
+        off[i] = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
+        res[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      for (int s0 = 0; s0 < a.splits; s0 += kSB) {
+        f32x4_t t[kPer][kSB];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+#pragma unroll
+          for (int j = 0; j < kSB; ++j) {
+            const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
+            const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(pres, off[i], (uint32_t)sj * sstride,
+                                                                     kCachePolicySC1);
+            // through plain scalars (hipcc 7.2 misreads a bit cast of a vector element)
+            const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+            t[i][j] = f32x4_t{__uint_as_float(e0), __uint_as_float(e1), __uint_as_float(e2), __uint_as_float(e3)};
+          }
+#pragma unroll
+        for (int i = 0; i < kPer; ++i)
+#pragma unroll
+          for (int j = 0; j < kSB; ++j) {
+            const bool live = s0 + j < a.splits;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) res[i][e] += live ? t[i][j][e] : 0.f;
+          }
+      }
+    }
   }
 
   // Slots to columns. Sequential order: slot = column. AutoAWQ: the even
@@ -551,23 +666,7 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, const float (*re
       v[3] = odd ? res[i][3] : x[1];
     }
     if (q >= kQ || m >= rows || n0 >= a.N) continue;
-    if (a.bias) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] += load_f32_any(a.bias, n0 + e, a.bt);
-    }
-    if (ACT) {
-      store_act_quad(a.y, a.yt, m, n0, a.N, v[0], v[1], v[2], v[3]);
-    } else if (a.yt == AWQ_F32) {
-      typedef float f4_t __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<f4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n0) = f4_t{v[0], v[1], v[2], v[3]};
-    } else if (a.yt == AWQ_F16) {
-      typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-      *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n0) =
-          h4_t{(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) store_out(a.y, a.yt, 0, m, n0 + e, a.N, v[e], 0.f);
-    }
+    store_cols4<ACT>(a, m, n0, v);
   }
 }
 
