@@ -400,6 +400,32 @@ def test_decode_rows_both_kernels(dev, monkeypatch, kernel, M, x_dt):
     assert oracle.rel_l2(to_host(y), ref) <= TOL_FP32
 
 
+@pytest.mark.parametrize("kernel,M,x_dt,y_dt,K", [
+    ("valu", 1, "f32", "f32", 9216),   # 8 waves x 32 rows: 36 splits, 4 thread groups
+    ("valu", 1, "f16", "f16", 14336),  # 16 waves x 32 rows: 28 splits, 8 thread groups
+    ("valu", 1, "bf16", "bf16", 9216),
+    ("valu", 2, "f32", "f32", 4096),   # 16 waves x 8 rows: 32 splits
+    ("m4", 3, "f16", "f32", 8192),     # 16 waves x 32 rows: 16 splits, 2 thread groups
+    ("m4", 4, "f16", "f16", 4608),     # 9 splits
+])
+def test_decode_deep_k_split_sum(dev, monkeypatch, kernel, M, x_dt, y_dt, K):
+    """More than 8 K splits: the last workgroup's sum over the splits is
+    shared by thread groups (contiguous split ranges, then the groups in a
+    fixed order). Partial column chunk, bias, each output type; two calls
+    give the same bits."""
+    for k, v in DECODE_KERNELS[kernel].items():
+        monkeypatch.setenv(k, v)
+    N, g = 2080, 128
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y1 = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", y_dt)
+    y2 = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", y_dt)
+    assert torch.equal(y1, y2)
+    got = host_f32(to_host(y1), y_dt)
+    assert np.isfinite(got).all()
+    tol = TOL_FP32 if y_dt == "f32" else (1e-3 if y_dt == "f16" else 5e-3)
+    assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= tol
+
+
 @pytest.mark.parametrize("waves,rpw", [(8, 64), (8, 32), (4, 64), (4, 32)])
 @pytest.mark.parametrize("s_dt", ["f32", "f16", "bf16"])
 def test_decode_mfma_every_configuration(dev, monkeypatch, waves, rpw, s_dt):

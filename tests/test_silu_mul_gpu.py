@@ -95,6 +95,29 @@ def test_silu_mul_every_route(dev, monkeypatch, M, x_dt, env):
     assert oracle.rel_l2(y, silu_mul64(full)) <= 2e-6
 
 
+@pytest.mark.parametrize("M,x_dt,K,env", [
+    (1, "f32", 9216, {}),                        # decode VALU, 36 K splits
+    (1, "f16", 14336, {}),                       # 28 K splits
+    (2, "f32", 4096, {"AWQ_DECODE_MFMA": "0"}),  # 2 rows, 32 K splits
+    (3, "f16", 8192, {}),                        # 4x4x4 blocks, 16 waves, 16 K splits
+])
+def test_silu_mul_decode_deep_k(dev, monkeypatch, M, x_dt, K, env):
+    """SiLU epilogue after a split-K sum over more than 8 splits (shared by
+    thread groups), with a partial column chunk and bias."""
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    N, g = 2112, 128  # a multiple of 64 (the gate/up rule), not of 512
+    s_dt = "f16"
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=s_dt, bias=True)
+    L = cube_awq.lib()
+    y = _launch(L.awq_gemm_silu_mul, dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, N // 2)
+    assert np.isfinite(y).all()
+    h = oracle.gemm_f64(host_f32(x, x_dt), qw, qz, host_f32(sc, s_dt), g, bias=b)
+    assert oracle.rel_l2(y, silu_mul64(h)) <= 2e-5
+    full = _launch(L.awq_gemm, dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, N)
+    assert oracle.rel_l2(y, silu_mul64(full)) <= 2e-6
+
+
 @pytest.mark.parametrize("M", [1, 5, 40, 200])
 def test_gate_up_module_matches_separate_layers(dev, M):
     """AWQGateUpSiLU.from_gate_up(gate, up)(x) == SiLU(gate(x)) * up(x)."""
