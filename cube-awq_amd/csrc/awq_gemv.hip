@@ -1057,8 +1057,8 @@ constexpr int rpw_max(int xt, int mt, int waves) {
 }
 
 // Rows per wave (dividing the group size) and waves per workgroup: enough
-// workgroups to occupy the CUs (>= 192) with as few K splits as possible,
-// since each split adds a partial round trip at the end; never a
+// workgroups to occupy the CUs with as few K splits as possible (one row:
+// one round of workgroups over the CUs where a shape allows it); never a
 // configuration that spills.
 template <int XT, int MT, int WMAX>
 void launch_rpw(const GemmProblem& p) {
@@ -1073,19 +1073,44 @@ void launch_rpw(const GemmProblem& p) {
     while (r > rpw_max(XT, MT, w)) r >>= 1;
     return r;
   };
-  while (waves > 4 && wgs(waves, cap(waves, rpw)) < 192) waves >>= 1;
-  // Small matrices keep more waves even below 192 workgroups: one row 8 waves
-  // of 32 rows (4 waves and twice the K splits measured 18-34 % slower at
-  // 4096 x 4096, 4096 x 1024 and 8192 x 1024: 8.35 / 7.96 / 11.2 us against
-  // 6.86 / 6.54 / 7.57; 16 waves 7-10 % slower), two rows 16 waves of 8
-  // (4096 x 1024: 12.8 us with 4 waves, 8.4 with 16).
-  if (MT == 1 && waves < 8 && WMAX >= 8 && rpw >= 32) waves = 8;
-  if (MT == 2) waves = WMAX;
-  rpw = cap(waves, rpw);
-  // Long runs per wave (fewer splits) while the workgroup count stays high.
-  while (rpw < 128 && 2 * rpw <= rpw_max(XT, MT, waves) && g % (2 * rpw) == 0 &&
-         wgs(waves, 2 * rpw) >= 192)
-    rpw *= 2;
+  if (MT == 1 && WMAX >= 16 && g % 32 == 0) {
+    // One row: one round of workgroups over the CUs (3/4 C .. C of them, C =
+    // CUs), since a partial second round finishes late. 16 waves x 32 rows
+    // when that gives such a round; fewer, shorter runs (down to 8 rows, more
+    // K splits) when it gives fewer; beyond C, 16 x 64 if that gives one
+    // round, else 8 waves x 32 rows (several rounds of small workgroups).
+    // Measured, us (one row, f32 x), chosen against the next best:
+    // 4096 -> 14336 / 14336 -> 4096 / 8192 -> 8192: 16 x 32 (224 / 224 / 256
+    // workgroups) 9.8 / 10.2 / 10.4 against 10.5 / 11.6 / 11.0 with 16 x 16;
+    // 4096 -> 4096 / 1024 -> 4096 / 8192 -> 1024: 16 x 8 6.3 / 5.2 / 6.7
+    // against 6.7 / 6.2 / 7.0 (16 x 16) and 6.8 / 6.5 / 7.4 (8 x 32);
+    // 4096 -> 6144: 16 x 16 7.3; 4096 -> 28672, 8192 -> 14336 and
+    // 14336 -> 8192: 16 x 64 (224) 17.1 / 17.1 / 17.3, 16 x 32 (448) up to
+    // 4 % slower; 5120 -> 13824 / 13824 -> 5120: 8 x 32 (540) 13.3 / 14.5
+    // against 15.9 / 16.3 with 16 x 32 (270); 8192 -> 28672 / 28672 -> 8192:
+    // 8 x 32 (1792) 29.1 / 30.2 against 31.3 / 31.6 with 16 x 64 (448).
+    const int64_t cus = device_cus(), lo = cus * 3 / 4;
+    waves = 16;
+    rpw = 32;
+    const int64_t w32 = wgs(16, 32);
+    if (w32 < lo) {
+      while (rpw > 8 && wgs(16, rpw) < lo) rpw >>= 1;
+    } else if (w32 > cus) {
+      const int64_t w64 = wgs(16, 64);
+      if (g % 64 == 0 && rpw_max(XT, 1, 16) >= 64 && w64 >= lo && w64 <= cus) rpw = 64;
+      else waves = 8;
+    }
+  } else {
+    while (waves > 4 && wgs(waves, cap(waves, rpw)) < 192) waves >>= 1;
+    // Small matrices keep more waves even below 192 workgroups: two rows 16
+    // waves of 8 (4096 x 1024: 12.8 us with 4 waves, 8.4 with 16).
+    if (MT == 2) waves = WMAX;
+    rpw = cap(waves, rpw);
+    // Long runs per wave (fewer splits) while the workgroup count stays high.
+    while (rpw < 128 && 2 * rpw <= rpw_max(XT, MT, waves) && g % (2 * rpw) == 0 &&
+           wgs(waves, 2 * rpw) >= 192)
+      rpw *= 2;
+  }
   if (int v = tuning(kTuneGemvWaves, 0); (v == 4 || v == 8 || v == 16) && v <= WMAX) waves = v;
   if (int v = tuning(kTuneGemvRpw, 0); v >= 4 && g % v == 0) rpw = v;
   rpw = cap(waves, rpw);
