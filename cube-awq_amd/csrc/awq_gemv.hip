@@ -1182,6 +1182,12 @@ void launch_mfma(const GemmProblem& p) {
   int waves = 8;
   if (rpw == 64 && wgs(8, 64) < 192) rpw = 32;
   if (rpw == 64 && MV <= 4 && wgs(8, 64) >= 2 * device_cus()) rpw = 32;
+  // 8 rows past one round of workgroups over the CUs: 4 waves x 64 rows
+  // (twice the workgroups, two per CU). 5120 -> 13824 / 8192 -> 28672 /
+  // 28672 -> 8192 (270 / 896 / 896 workgroups of 8 x 64): 29.3 / 55.4 / 60.2
+  // -> 25.7 / 49.3 / 57.3 us; within one round (224, 256) 4 x 64 measured
+  // 13-18 % slower.
+  if (MV == 8 && rpw == 64 && wgs(8, 64) > device_cus()) waves = 4;
   if (int v = tuning(kTuneMfmaWaves, 0); v == 4 || v == 8) waves = v;
   if (int v = tuning(kTuneMfmaRpw, 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
   if (waves == 8 && rpw == 64) return launch_mfma_cfg<XT, MV, 8, 64>(p);
@@ -1226,20 +1232,27 @@ void launch_m4_cfg(const GemmProblem& p) {
   check_hip(hipGetLastError(), "gemv m4 kernel launch");
 }
 
-// 4x4x4 matrix-core decode: 16 waves x 32 rows for 4 rows of f16
-// activations (the only case whose registers, <= 128 VGPRs, and LDS slots,
-// 16 x 4 rows x 2 KB, allow 16 waves); otherwise 8 waves of 64 rows when
-// that gives 192..511 workgroups (and the group allows 64), else 8 x 32.
-// Measured with f32 activations at 2..4 rows: 64 rows at 4096 -> 14336 and
-// 14336 -> 4096 (224 workgroups) 5-12 % faster than 32; 32 rows where 64
-// gives 64 or >= 896 workgroups (4096 -> 4096, 28672 -> 8192) 10-15 % faster.
+// 4x4x4 matrix-core decode. 512 rows per workgroup (16 waves x 32 rows, or
+// 8 x 64) when that gives one round of workgroups over the CUs (3/4 C .. C,
+// C = CUs): 16 x 32 for f16 activations (the only case whose registers,
+// <= 128 VGPRs, and LDS slots, 16 x 4 rows x 2 KB, allow 16 waves), else
+// 8 x 64 (if the group allows 64); otherwise 8 waves of 32 rows. Measured at
+// 4 rows, us: 8 x 64 at 4096 -> 14336 / 14336 -> 4096 (224 workgroups) 5-12 %
+// faster than 8 x 32 with f32 activations, 16 x 32 at 14336 -> 4096 /
+// 8192 -> 8192 (224 / 256) 13.4 / 12.6 against 15.0 / 13.3 with 8 waves for
+// f16; 8 x 32 where 512 rows give a partial or several rounds: 5120 -> 13824
+// / 13824 -> 5120 (270) f32 25.3 / 26.3 -> 19.9 / 21.0 (against 8 x 64),
+// f16 19.3 / 20.2 -> 15.8 / 17.9 (against 16 x 32); 8192 -> 28672 (896) f16
+// 38.1 -> 33.7; 4096 -> 4096 (64) f16 10.0 -> 8.3.
 template <int XT, int MV>
 void launch_m4(const GemmProblem& p) {
   constexpr bool k16 = MV == 4 && XT == AWQ_F16;
   const int64_t chunks = (p.N / 8 + 63) / 64;
   const int64_t wgs64 = chunks * ((p.K + 511) / 512);
-  int waves = k16 ? 16 : 8;
-  int rpw = (!k16 && p.group % 64 == 0 && wgs64 >= 192 && wgs64 < 512) ? 64 : 32;
+  const int64_t cus = device_cus();
+  const bool one_round = wgs64 >= cus * 3 / 4 && wgs64 <= cus;
+  int waves = k16 && one_round ? 16 : 8;
+  int rpw = (waves == 8 && p.group % 64 == 0 && one_round) ? 64 : 32;
   if (int v = tuning(kTuneM4Waves, 0); v == 8 || (v == 16 && k16)) waves = v;
   if (int v = tuning(kTuneM4Rpw, 0); (v == 32 || v == 64) && p.group % v == 0) rpw = v;
   if constexpr (k16) {
