@@ -275,6 +275,7 @@ enum TuneKey {
   kTuneSkinny,        // AWQ_SKINNY
   kTuneSkinnySplits,  // AWQ_SKINNY_SPLITS
   kTuneSkinnyCols,    // AWQ_SKINNY_COLS
+  kTuneDecodeTree,    // AWQ_DECODE_TREE
   kTuneCount
 };
 // The override's value (atoi of the variable), or dflt when it is unset.

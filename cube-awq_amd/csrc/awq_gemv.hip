@@ -55,13 +55,15 @@ struct GemvArgs {
   const void* scales;
   const void* bias;
   void* y;
-  float* partial;     // [splits][MT][N] when splits > 1
-  uint32_t* counters; // one per chunk, kCounterStride apart, zero between calls
+  float* partial;     // [splits (+ ngroups)][MT][N] when splits > 1
+  uint32_t* counters; // per chunk (ngroups + 1 with the tree), kCounterStride apart, zero between calls
   int32_t st, bt, yt;
   int32_t rows;       // valid rows (<= MT)
   int32_t K, N, group;
   int32_t splits;
   int32_t seq;        // sequential nibble order (packed lane j = column j)
+  int32_t gsize;      // two-level split sum: splits per group (finish_chunk, when ngroups > 1)
+  int32_t ngroups;    // groups of gsize splits; 0 or 1: one level
 };
 
 template <int XT>
@@ -146,25 +148,33 @@ __device__ __forceinline__ void fma_word(float (&acc)[8], float x, const h2_t (&
 
 constexpr int kCounterStride = 64;  // u32 words between arrival counters (256 B)
 
+// Partial planes of the split-K workspace: one per split, plus one per group
+// with the two-level sum.
+__device__ __forceinline__ int partial_planes(const GemvArgs& a) {
+  return a.splits + (a.ngroups > 1 ? a.ngroups : 0);
+}
+
 // Split-K sums with more splits than a single batch of loads: the last
 // workgroup of a chunk sums the partials of its kQ 4-column pieces with kG
 // thread groups (threads kG * kQ of the workgroup; piece q = tid % kQ, group
-// h = tid / kQ, uniform per wave since kQ is a multiple of 64). Group h sums
-// splits [h per, (h + 1) per) in order with all of its 16-byte loads in
-// flight; the kG group sums meet in lds (kG * kQ 16-byte entries) and are
-// added in group order. Returns the piece's total in threads tid < kQ; every
-// thread of the workgroup calls it (it holds a barrier). The partials are
-// laid out [split][MV][N] f32, columns in order.
+// h = tid / kQ, uniform per wave since kQ is a multiple of 64). Of the np
+// planes from p0 (of `planes` in the workspace), group h sums [h per,
+// (h + 1) per) in order with all of its 16-byte loads in flight; the kG
+// group sums meet in lds (kG * kQ 16-byte entries) and are added in group
+// order. Returns the piece's total in threads tid < kQ; every thread of the
+// workgroup calls it (it holds a barrier). The partials are laid out
+// [plane][MV][N] f32.
 template <int MV, int kQ, int kG>
-__device__ __forceinline__ f32x4_t grouped_split_sum(const GemvArgs& a, f32x4_t* lds, int rows, int col_base) {
+__device__ __forceinline__ f32x4_t grouped_split_sum(const GemvArgs& a, f32x4_t* lds, int rows, int col_base,
+                                                     int planes, int p0, int np) {
   const int tid = threadIdx.x;
   const int q = tid % kQ, h = tid / kQ;
   const int m = q / 128, c0 = 4 * (q % 128);
-  const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * MV * a.N * 4));
+  const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)planes * MV * a.N * 4));
   const uint32_t sstride = (uint32_t)((int64_t)MV * a.N * 4);
   const uint32_t off = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
-  const int per = (a.splits + kG - 1) / kG;
-  const int sb = min(h * per, a.splits), se = min(sb + per, a.splits);
+  const int per = (np + kG - 1) / kG;
+  const int sb = p0 + min(h * per, np), se = min(sb + per, p0 + np);
   f32x4_t v = f32x4_t{0.f, 0.f, 0.f, 0.f};
   auto run = [&](auto nb) {
     constexpr int NB = decltype(nb)::value;
@@ -409,7 +419,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
       if (a.splits > 8) {
         // The slots are free: every thread read its slots before the arrival barrier.
         const f32x4_t r = grouped_split_sum<MT, kQ, 64 * WAVES / kQ>(
-            a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base);
+            a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base, a.splits, 0, a.splits);
         const int q = threadIdx.x;
         const int m = q / (kChunkCols / 4), n0 = col_base + 4 * (q % (kChunkCols / 4));
         if (q < kQ && m < rows && n0 < a.N) {
@@ -567,78 +577,108 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, float (*red)[MV]
 
   if (a.splits > 1) {
     // Same handshake as the VALU path, with sc1 buffer stores and loads
-    // (split-K handshake, awq_common.h); the last workgroup sums the splits
-    // in order.
-    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * MV * a.N * 4));
+    // (split-K handshake, awq_common.h). One level: the last workgroup of
+    // the chunk sums the splits in order. Two levels (ngroups > 1, deep K):
+    // the splits form groups of gsize; the last workgroup of a group sums
+    // the group's splits in order and publishes that sum as plane splits +
+    // group through the same handshake, and the last group sums the group
+    // planes in order. Both orders are fixed, so results stay deterministic;
+    // the last workgroup's serial sum (bound by one CU's loads) shrinks from
+    // splits planes to about 2 sqrt(splits).
+    const bool tree = a.ngroups > 1;
+    const int cpc = tree ? a.ngroups + 1 : 1;  // counters per chunk
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)partial_planes(a) * MV * a.N * 4));
     const uint32_t sstride = (uint32_t)((int64_t)MV * a.N * 4);
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-      const int q = tid + i * kTh;
-      const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
-      if (q < kQ && m < rows && col_base + c0 < a.N) {
-        const float f0 = res[i][0], f1 = res[i][1], f2 = res[i][2], f3 = res[i][3];
-        const u32x4_t w4 = u32x4_t{__float_as_uint(f0), __float_as_uint(f1), __float_as_uint(f2), __float_as_uint(f3)};
-        __builtin_amdgcn_raw_buffer_store_b128(w4, pres, (uint32_t)(((int64_t)m * a.N + col_base + c0) * 4),
-                                               (uint32_t)split * sstride, kCachePolicySC1);
-      }
-    }
-    // Partials complete before the arrival (split-K handshake, awq_common.h).
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCounterStride], 1u,
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!s_last) return;
-    if (tid == 0)
-      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    bool grouped = false;
-    if constexpr (kG > 1) grouped = a.splits > 8;
-    if (grouped) {
-      // More threads than pieces and more than 8 splits: one round of loads
-      // shared by kG thread groups (the slots are free: every thread read its
-      // slots before the arrival barrier).
-      if constexpr (kG > 1)
-        res[0] = grouped_split_sum<MV, kQ, kG>(a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base);
-    } else {
-      // Each thread's kPer pieces, kSB splits at a time: kPer * kSB loads in
-      // flight; every output still sums its splits in order.
-      constexpr int kSB = kPer >= 4 ? 4 : 8;
-      uint32_t off[kPer];
+    auto store_plane = [&](int plane) {
 #pragma unroll
       for (int i = 0; i < kPer; ++i) {
-        const int q = min(tid + i * kTh, kQ - 1);
+        const int q = tid + i * kTh;
         const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
-        // Rows past M read row M-1's partials (cached, discarded): unconditional
-        // loads keep the batch in flight.
-        off[i] = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
-        res[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        if (q < kQ && m < rows && col_base + c0 < a.N) {
+          const float f0 = res[i][0], f1 = res[i][1], f2 = res[i][2], f3 = res[i][3];
+          const u32x4_t w4 =
+              u32x4_t{__float_as_uint(f0), __float_as_uint(f1), __float_as_uint(f2), __float_as_uint(f3)};
+          __builtin_amdgcn_raw_buffer_store_b128(w4, pres, (uint32_t)(((int64_t)m * a.N + col_base + c0) * 4),
+                                                 (uint32_t)plane * sstride, kCachePolicySC1);
+        }
       }
-      for (int s0 = 0; s0 < a.splits; s0 += kSB) {
-        f32x4_t t[kPer][kSB];
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-#pragma unroll
-          for (int j = 0; j < kSB; ++j) {
-            const int sj = min(s0 + j, a.splits - 1);  // clamped: stays in the workspace
-            const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(pres, off[i], (uint32_t)sj * sstride,
-                                                                     kCachePolicySC1);
-            // through plain scalars (hipcc 7.2 misreads a bit cast of a vector element)
-            const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
-            t[i][j] = f32x4_t{__uint_as_float(e0), __uint_as_float(e1), __uint_as_float(e2), __uint_as_float(e3)};
-          }
-#pragma unroll
-        for (int i = 0; i < kPer; ++i)
-#pragma unroll
-          for (int j = 0; j < kSB; ++j) {
-            const bool live = s0 + j < a.splits;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) res[i][e] += live ? t[i][j][e] : 0.f;
-          }
+    };
+    // Publish the stored plane and count the arrival on counter ci of this
+    // chunk; true in the last of `expect` arrivals (which re-arms it).
+    auto arrive = [&](int ci, int expect) -> bool {
+      // Partials complete before the arrival (split-K handshake, awq_common.h).
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      uint32_t* ctr = &a.counters[(chunk * cpc + ci) * kCounterStride];
+      if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = (prev == (uint32_t)(expect - 1)) ? 1 : 0;
       }
+      __syncthreads();
+      if (!s_last) return false;
+      if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return true;
+    };
+    // res = the sum of planes p0 .. p0 + np - 1, in order.
+    auto sum_planes = [&](int p0, int np) {
+      bool grouped = false;
+      if constexpr (kG > 1) grouped = np > 8;
+      if (grouped) {
+        // More threads than pieces and more than 8 planes: one round of
+        // loads shared by kG thread groups (the slots are free: every thread
+        // read its slots before the first arrival barrier).
+        if constexpr (kG > 1)
+          res[0] = grouped_split_sum<MV, kQ, kG>(a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base,
+                                                 partial_planes(a), p0, np);
+      } else {
+        // Each thread's kPer pieces, kSB planes at a time: kPer * kSB loads
+        // in flight; every output still sums its planes in order.
+        constexpr int kSB = kPer >= 4 ? 4 : 8;
+        uint32_t off[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const int q = min(tid + i * kTh, kQ - 1);
+          const int m = q / (kChunkCols / 4), c0 = 4 * (q % (kChunkCols / 4));
+          // Rows past M read row M-1's partials (cached, discarded): unconditional
+          // loads keep the batch in flight.
+          off[i] = (uint32_t)(((int64_t)min(m, rows - 1) * a.N + min(col_base + c0, a.N - 4)) * 4);
+          res[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        for (int s0 = 0; s0 < np; s0 += kSB) {
+          f32x4_t t[kPer][kSB];
+#pragma unroll
+          for (int i = 0; i < kPer; ++i)
+#pragma unroll
+            for (int j = 0; j < kSB; ++j) {
+              const int sj = p0 + min(s0 + j, np - 1);  // clamped: stays in the range
+              const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(pres, off[i], (uint32_t)sj * sstride,
+                                                                       kCachePolicySC1);
+              // through plain scalars (hipcc 7.2 misreads a bit cast of a vector element)
+              const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+              t[i][j] = f32x4_t{__uint_as_float(e0), __uint_as_float(e1), __uint_as_float(e2), __uint_as_float(e3)};
+            }
+#pragma unroll
+          for (int i = 0; i < kPer; ++i)
+#pragma unroll
+            for (int j = 0; j < kSB; ++j) {
+              const bool live = s0 + j < np;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) res[i][e] += live ? t[i][j][e] : 0.f;
+            }
+        }
+      }
+    };
+    store_plane(split);
+    if (tree) {
+      const int grp = split / a.gsize, gbeg = grp * a.gsize, gn = min(a.gsize, a.splits - gbeg);
+      if (!arrive(grp, gn)) return;
+      sum_planes(gbeg, gn);
+      store_plane(a.splits + grp);
+      if (!arrive(a.ngroups, a.ngroups)) return;
+      sum_planes(a.splits, a.ngroups);
+    } else {
+      if (!arrive(0, a.splits)) return;
+      sum_planes(0, a.splits);
     }
   }
 
@@ -1006,6 +1046,41 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_m4_kernel(GemvArgs a) {
   finish_chunk<MV, WAVES, WAVES, ACT>(a, red, &s_last, rows, seq);
 }
 
+// Two-level split sum of the matrix-core decode kernels (finish_chunk): groups
+// of g splits (the smallest g with g * g >= splits) where the last
+// workgroups' serial sums (splits planes of MV x 2 KB, bound by one CU's
+// loads) end the call: 24 or more splits over at most 16 column chunks (and
+// 4 or more at 4 rows). Measured (us, one level / two, f32 x): 8 rows
+// 14336 -> 4096 / 13824 -> 5120 / 28672 -> 8192 / 8192 -> 1024 (28 / 54 /
+// 112 / 32 splits) 20.4 / 31.0 / 57.6 / 15.0 -> 19.6 / 27.4 / 51.1 / 14.2;
+// 4 rows on the first three 16.8 / 21.2 / 44.5 -> 16.3 / 20.0 / 43.9; 12 and
+// 16 rows 14336 -> 4096 / 28672 -> 8192 25.5 / 75.5 -> 23.5 / 66.6. Slower
+// at 16 or 20 splits (3-17 %), on 56 chunks (8192 -> 28672, 32 splits:
+// 3 %) and at 4 rows over 2 chunks (3 %). AWQ_DECODE_TREE=0 / 1 forces one
+// level / two (3 or more splits). Then the split-K workspace: partial
+// planes and arrival counters.
+void set_split_sum(const GemmProblem& p, GemvArgs& a, int mv, int chunks) {
+  a.gsize = a.splits;
+  a.ngroups = 1;
+  const int force = tuning(kTuneDecodeTree, -1);
+  const bool deep = a.splits >= 24 && chunks <= 16 && (mv >= 8 || chunks >= 4);
+  if (force != 0 && a.splits >= 3 && (force == 1 || deep)) {
+    int g = 1;
+    while (g * g < a.splits) ++g;
+    const int ng = (a.splits + g - 1) / g;
+    if (ng > 1) {
+      a.gsize = g;
+      a.ngroups = ng;
+    }
+  }
+  const int planes = a.splits + (a.ngroups > 1 ? a.ngroups : 0);
+  const int cpc = a.ngroups > 1 ? a.ngroups + 1 : 1;
+  const size_t part_bytes = (size_t)planes * mv * p.N * sizeof(float);
+  const size_t ctr_bytes = (size_t)chunks * cpc * kCounterStride * sizeof(uint32_t);
+  a.counters = static_cast<uint32_t*>(ws_get(p, ctr_bytes, kWsCounters));
+  a.partial = static_cast<float*>(ws_get(p, part_bytes, kWsPartials));
+}
+
 template <int XT, int MT, int WAVES, int RPW>
 void launch_cfg(const GemmProblem& p) {
   const int np = (int)(p.N / 8);
@@ -1149,12 +1224,7 @@ void launch_mfma_cfg(const GemmProblem& p) {
   a.group = (int32_t)p.group;
   a.splits = splits;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
-  if (splits > 1) {
-    const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
-    const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
-    a.counters = static_cast<uint32_t*>(ws_get(p, ctr_bytes, kWsCounters));
-    a.partial = static_cast<float*>(ws_get(p, part_bytes, kWsPartials));
-  }
+  if (splits > 1) set_split_sum(p, a, MV, chunks);
   if (p.act)
     hipLaunchKernelGGL((gemv_mfma_kernel<XT, MV, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES),
                        0, p.stream, a);
@@ -1217,12 +1287,7 @@ void launch_m4_cfg(const GemmProblem& p) {
   a.group = (int32_t)p.group;
   a.splits = splits;
   a.seq = p.order == AWQ_ORDER_SEQUENTIAL ? 1 : 0;
-  if (splits > 1) {
-    const size_t part_bytes = (size_t)splits * MV * p.N * sizeof(float);
-    const size_t ctr_bytes = (size_t)chunks * kCounterStride * sizeof(uint32_t);
-    a.counters = static_cast<uint32_t*>(ws_get(p, ctr_bytes, kWsCounters));
-    a.partial = static_cast<float*>(ws_get(p, part_bytes, kWsPartials));
-  }
+  if (splits > 1) set_split_sum(p, a, MV, chunks);
   if (p.act)
     hipLaunchKernelGGL((gemv_m4_kernel<XT, MV, WAVES, RPW, true>), dim3(chunks, splits), dim3(64 * WAVES), 0,
                        p.stream, a);

@@ -426,6 +426,44 @@ def test_decode_deep_k_split_sum(dev, monkeypatch, kernel, M, x_dt, y_dt, K):
     assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= tol
 
 
+@pytest.mark.parametrize("kernel,M,x_dt,K,g", [
+    ("m4", 2, "f32", 8192, 128),      # 8 waves x 32 rows: 32 splits, groups of 6 (the last of 2)
+    ("m4", 4, "f16", 14336, 128),     # 56 splits, groups of 8
+    ("m4", 3, "bf16", 4160, 64),      # 17 splits, the last wave of the last past K
+    ("mfma16", 3, "f32", 9216, 128),  # 4-row tile: 36 splits, groups of 6
+    ("mfma16", 8, "f16", 14336, 128), # 8 x 32 rows: 56 splits, groups of 8
+    ("mfma16", 6, "bf16", 6144, 64),  # 24 splits, groups of 5 (the last of 4)
+])
+@pytest.mark.parametrize("tree", ["0", "1"])
+def test_decode_split_sum_levels(dev, monkeypatch, kernel, M, x_dt, K, g, tree):
+    """The matrix-core decode kernels' split-K sum in one level (the last
+    workgroup sums every split) and in two (groups of splits, then the
+    groups), each against the oracle, with bias and a partial column chunk;
+    two calls give the same bits."""
+    for k, v in DECODE_KERNELS[kernel].items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.setenv("AWQ_DECODE_TREE", tree)
+    N = 2080
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y1 = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32")
+    y2 = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32")
+    assert torch.equal(y1, y2)
+    got = to_host(y1)
+    assert np.isfinite(got).all()
+    assert oracle.rel_l2(got, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_FP32
+
+
+@pytest.mark.parametrize("M,x_dt", [(12, "f32"), (16, "f32")])
+def test_small_m_split_sum_two_levels(dev, monkeypatch, M, x_dt):
+    """9..16 rows on the 16-row decode tile with the two-level split sum."""
+    monkeypatch.setenv("AWQ_DECODE_TREE", "1")
+    K, N, g = 8192, 1056, 128
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, "f16", "f32"))
+    assert np.isfinite(y).all()
+    assert oracle.rel_l2(y, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_FP32
+
+
 @pytest.mark.parametrize("waves,rpw", [(8, 64), (8, 32), (4, 64), (4, 32)])
 @pytest.mark.parametrize("s_dt", ["f32", "f16", "bf16"])
 def test_decode_mfma_every_configuration(dev, monkeypatch, waves, rpw, s_dt):

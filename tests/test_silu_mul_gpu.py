@@ -100,6 +100,8 @@ def test_silu_mul_every_route(dev, monkeypatch, M, x_dt, env):
     (1, "f16", 14336, {}),                       # 28 K splits
     (2, "f32", 4096, {"AWQ_DECODE_MFMA": "0"}),  # 2 rows, 32 K splits
     (3, "f16", 8192, {}),                        # 4x4x4 blocks, 16 waves, 16 K splits
+    (4, "f32", 14336, {"AWQ_DECODE_TREE": "1"}),   # 4x4x4 blocks, two-level split sum
+    (8, "f16", 14336, {"AWQ_DECODE_TREE": "1"}),   # 16-row tile, two-level split sum
 ])
 def test_silu_mul_decode_deep_k(dev, monkeypatch, M, x_dt, K, env):
     """SiLU epilogue after a split-K sum over more than 8 splits (shared by
