@@ -60,6 +60,22 @@ def test_sequential_matches_oracle_and_autoawq_bits(dev, M, dt):
     assert oracle.rel_l2(y_seq, ref) <= tol
 
 
+@pytest.mark.parametrize("M,dt", [(1, "f32"), (4, "f32"), (8, "f16"), (12, "f32")])
+def test_sequential_deep_k_split_sums(dev, monkeypatch, M, dt):
+    """Deep K on the decode kernels (36..72 K splits): the grouped one-row sum
+    and, forced here, the two-level sum of the matrix-core kernels, in
+    sequential order against AutoAWQ order (same bits) and the oracle."""
+    monkeypatch.setenv("AWQ_DECODE_TREE", "1")
+    K, N, g = 9216, 1056, 128
+    x, qw_awq, qz_awq, sc, b = make_problem(M, K, N, g, x_dt=dt, s_dt=dt, bias=True)
+    qw_seq, qz_seq = _to_seq(qw_awq), _to_seq(qz_awq)
+    y_seq = _run(dev, x, qw_seq, qz_seq, sc, b, M, K, N, g, dt, _lib.AWQ_ORDER_SEQUENTIAL, "f32")
+    y_awq = _run(dev, x, qw_awq, qz_awq, sc, b, M, K, N, g, dt, _lib.AWQ_ORDER_AUTOAWQ, "f32")
+    assert np.array_equal(y_seq.view(np.uint32), y_awq.view(np.uint32))
+    ref = oracle.gemm_f64(host_f32(x, dt), qw_seq, qz_seq, host_f32(sc, dt), g, bias=b, order="seq")
+    assert oracle.rel_l2(y_seq, ref) <= TOL_FP32
+
+
 @pytest.mark.parametrize("tile", [1, 2, 3, 4, 6, 7, 8, 9, 10, 11, 12])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 def test_sequential_every_tile_configuration(dev, monkeypatch, tile, dt):
