@@ -687,7 +687,11 @@ void launch_rows_cw(const GemmProblem& p) {
   if (p.rows <= 32) return launch_mt<2, BF, CW, WV>(p);
   if (p.rows <= 48) return launch_mt<3, BF, CW, WV>(p);
   if (p.rows <= 64) return launch_mt<4, BF, CW, WV>(p);
+  // 5 and 7 tiles for 65..80 and 97..112 rows (against 6 and 8: 2-5 %
+  // faster, e.g. 4096 -> 14336 at M = 72 / 100 27.6 / 32.1 -> 26.4 / 31.0 us).
+  if (p.rows <= 80) return launch_mt<5, BF, CW, WV>(p);
   if (p.rows <= 96) return launch_mt<6, BF, CW, WV>(p);
+  if (p.rows <= 112) return launch_mt<7, BF, CW, WV>(p);
   return launch_mt<8, BF, CW, WV>(p);
 }
 
