@@ -247,8 +247,9 @@ void launch_gemm(const GemmProblem& p);   // rows > 8
 // 9..16 rows run on the matrix-core decode kernel (16-row tile) when its
 // constraints hold (group % 32, K % 32); AWQ_SMALLM_MFMA=0 turns it off.
 bool small_m_mfma_ok(const GemmProblem& p, int64_t launch_m);
-// 17..128 rows of f16 activations on wide outputs: the skinny kernel
-// (awq_skinny.hip); AWQ_SKINNY=0/1 forces the choice.
+// 9..128 rows of f16/bf16 activations (wide outputs, or narrower ones up
+// to 64..128 rows): the skinny kernel (awq_skinny.hip); AWQ_SKINNY=0/1
+// forces the choice.
 bool skinny_ok(const GemmProblem& p);
 void launch_skinny(const GemmProblem& p);
 

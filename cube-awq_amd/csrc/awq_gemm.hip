@@ -36,7 +36,8 @@
 //    XCD runs a contiguous block of them, sharing X and W in its L2.
 //  * Problems with fewer tiles than CUs split K across workgroups; partials
 //    are summed in split order by the last workgroup to arrive on its tile.
-//    (17..128 rows on wide outputs take the skinny kernel, awq_skinny.hip.)
+//    (9..128 rows of f16/bf16 take the skinny kernel where it is faster,
+//    awq_skinny.hip.)
 // gemm_kernel (generic, 128x128, padded LDS, VGPR-staged loads) takes fp32
 // activations (v_mfma_f32_32x32x2_f32, W dequantised in f32 exactly as the
 // reference's F = f32 kernel) and every shape the large-tile kernel does not.

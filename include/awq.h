@@ -12,7 +12,7 @@
  * (splits x rows x N x 4 bytes) and arrival counters (<= 256 bytes per
  * column chunk or tile) in a workspace owned by the library, one per
  * (device, stream). Routes that split K: the decode kernels (M <= 16) when K
- * spans more than one workgroup's rows, the 17..128-row kernel, the
+ * spans more than one workgroup's rows, the 9..128-row f16/bf16 kernel, the
  * large-tile kernel when it has few tiles (about M <= 1024), and fp32
  * activations run as 16-row slices. The workspace is allocated on first need
  * and grown when a call needs more; a superseded buffer is never freed (it is
