@@ -121,7 +121,7 @@ static const char* const kTuneNames[kTuneCount] = {
     "AWQ_GEMM_TILE",  "AWQ_GEMM_SPLITS", "AWQ_GEMM_GROUP_M", "AWQ_F32_SLICES",  "AWQ_GEMV_WAVES",
     "AWQ_GEMV_RPW",   "AWQ_MFMA_WAVES",  "AWQ_MFMA_RPW",     "AWQ_M4_WAVES",    "AWQ_M4_RPW",
     "AWQ_DECODE_MFMA", "AWQ_DECODE_M4",  "AWQ_SMALLM_MFMA",  "AWQ_SKINNY",      "AWQ_SKINNY_SPLITS",
-    "AWQ_SKINNY_COLS", "AWQ_DECODE_TREE"};
+    "AWQ_SKINNY_COLS", "AWQ_DECODE_TREE", "AWQ_SKINNY_TREE"};
 static std::atomic<int> g_tune_val[kTuneCount];
 static std::atomic<bool> g_tune_set[kTuneCount];
 static std::once_flag g_tune_once;

@@ -277,6 +277,7 @@ enum TuneKey {
   kTuneSkinnySplits,  // AWQ_SKINNY_SPLITS
   kTuneSkinnyCols,    // AWQ_SKINNY_COLS
   kTuneDecodeTree,    // AWQ_DECODE_TREE
+  kTuneSkinnyTree,    // AWQ_SKINNY_TREE
   kTuneCount
 };
 // The override's value (atoi of the variable), or dflt when it is unset.

@@ -97,14 +97,16 @@ struct SkinnyArgs {
   const void* scales;
   const void* bias;
   void* y;
-  float* partial;      // [splits][M][N] when splits > 1
-  uint32_t* counters;  // one per chunk, kCtrStride apart, zero between calls
+  float* partial;      // [splits (+ ngroups)][M][N] when splits > 1
+  uint32_t* counters;  // per chunk (ngroups + 1 with the two-level sum), kCtrStride apart, zero between calls
   int32_t st, bt, yt;
   int32_t M, K, N, group;
   int32_t splits, steps_per_split;
   int32_t seq;         // sequential nibble order
   int32_t chunks;      // column chunks (grid.x)
   int32_t xcd_chunks;  // leading chunks covered by the XCD mapping (multiple of 8)
+  int32_t gsize;       // two-level split sum: splits per group (when ngroups > 1)
+  int32_t ngroups;     // groups of gsize splits; 0 or 1: one level
 };
 
 constexpr int waitcnt_vm(int vm) { return (vm & 0xF) | ((vm >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -430,7 +432,8 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
   // 8 (chunk kPacks + pl) + colt[t] ----------------------------------------------
   const int nbase = chunk * CW + 8 * pl;
   if (a.splits > 1) {
-    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)a.splits * a.M * a.N * 4));
+    const int planes = a.splits + (a.ngroups > 1 ? a.ngroups : 0);
+    const rsrc_t pres = make_rsrc(a.partial, (uint32_t)((int64_t)planes * a.M * a.N * 4));
     constexpr int kQuads = CW / 4;
     // 256-column chunks stage the partial tile in LDS (idle once every wave
     // has left the main loop) and store it as whole 16-byte row pieces with
@@ -480,90 +483,121 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
                                  __HIP_MEMORY_SCOPE_AGENT);
           }
     }
-    // Partials complete before the arrival (split-K handshake, awq_common.h).
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (tid == 0) {
-      const uint32_t prev = __hip_atomic_fetch_add(&a.counters[chunk * kCtrStride], 1u, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-      *s_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!*s_last) return;
-    // Sum the splits of this chunk in split order: 4 consecutive columns per
-    // 16-byte load (N % 32 == 0 keeps them inside a row), kG column groups
-    // per thread per round, kSB splits deep -- kG kSB loads in flight, so
-    // most chunks take one round. Slots past the chunk, M or the splits are
-    // loaded clamped and not used.
+    // One level: the last workgroup of the chunk sums the splits in order.
+    // Two levels (ngroups > 1, deep K): the splits form groups of gsize; the
+    // last workgroup of a group sums the group's splits in order and
+    // publishes that sum as plane splits + group through the same handshake
+    // (one more arrival counter per group), and the last group sums the
+    // group planes in order. Both trees are fixed, so results stay
+    // deterministic.
+    const bool tree = a.ngroups > 1;
+    const int cpc = tree ? a.ngroups + 1 : 1;  // counters per chunk
+    auto arrive = [&](int ci, int expect) -> bool {
+      // Partials complete before the arrival (split-K handshake, awq_common.h).
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      uint32_t* ctr = &a.counters[(chunk * cpc + ci) * kCtrStride];
+      if (tid == 0) {
+        const uint32_t prev = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *s_last = (prev == (uint32_t)(expect - 1)) ? 1 : 0;
+      }
+      __syncthreads();
+      if (!*s_last) return false;
+      if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return true;
+    };
+    // Sum planes p0 .. p0 + np - 1 of this chunk in order: 4 consecutive
+    // columns per 16-byte load (N % 32 == 0 keeps them inside a row), kG
+    // column groups per thread per round, kSB planes deep -- kG kSB loads in
+    // flight, so most chunks take one round. Slots past the chunk, M or the
+    // planes are loaded clamped and not used. The sums go to plane
+    // out_plane (>= 0) or, with the bias and epilogue, to Y.
     const uint32_t sstride = (uint32_t)((int64_t)a.M * a.N * 4);
     constexpr int kG = 4, kSB = 4;
     constexpr int kTh = C::kThreads;
     const int total4 = a.M * kQuads;
-    for (int base = 0; base < total4; base += kTh * kG) {
-      uint32_t off[kG];
-      bool ok[kG];
-      float v[kG][4];
+    auto reduce = [&](int p0, int np, int out_plane) {
+      for (int base = 0; base < total4; base += kTh * kG) {
+        uint32_t off[kG];
+        bool ok[kG];
+        float v[kG][4];
 #pragma unroll
-      for (int g = 0; g < kG; ++g) {
-        const int e4 = base + g * kTh + tid;
-        const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
-        ok[g] = e4 < total4 && n < a.N;
-        off[g] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 4)) * 4);
+        for (int g = 0; g < kG; ++g) {
+          const int e4 = base + g * kTh + tid;
+          const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
+          ok[g] = e4 < total4 && n < a.N;
+          off[g] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 4)) * 4);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) v[g][q] = 0.f;
-      }
-      for (int sp = 0; sp < a.splits; sp += kSB) {
-        float t[kG][kSB][4];
+          for (int q = 0; q < 4; ++q) v[g][q] = 0.f;
+        }
+        for (int sp = 0; sp < np; sp += kSB) {
+          float t[kG][kSB][4];
 #pragma unroll
-        for (int g = 0; g < kG; ++g)
+          for (int g = 0; g < kG; ++g)
 #pragma unroll
-          for (int b = 0; b < kSB; ++b) {
-            const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(
-                pres, off[g], (uint32_t)min(sp + b, a.splits - 1) * sstride, kCachePolicySC1);
-            // through plain scalars: __builtin_bit_cast of a vector element
-            // directly reads the wrong element (hipcc 7.2)
-            const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
-            t[g][b][0] = __uint_as_float(e0);
-            t[g][b][1] = __uint_as_float(e1);
-            t[g][b][2] = __uint_as_float(e2);
-            t[g][b][3] = __uint_as_float(e3);
+            for (int b = 0; b < kSB; ++b) {
+              const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(
+                  pres, off[g], (uint32_t)(p0 + min(sp + b, np - 1)) * sstride, kCachePolicySC1);
+              // through plain scalars: __builtin_bit_cast of a vector element
+              // directly reads the wrong element (hipcc 7.2)
+              const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+              t[g][b][0] = __uint_as_float(e0);
+              t[g][b][1] = __uint_as_float(e1);
+              t[g][b][2] = __uint_as_float(e2);
+              t[g][b][3] = __uint_as_float(e3);
+            }
+#pragma unroll
+          for (int g = 0; g < kG; ++g)
+#pragma unroll
+            for (int b = 0; b < kSB; ++b) {
+              const bool live = sp + b < np;
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[g][q] += live ? t[g][b][q] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          if (!ok[g]) continue;
+          const int e4 = base + g * kTh + tid;
+          const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
+          if (out_plane >= 0) {
+            const u32x4_t w4 = u32x4_t{__float_as_uint(v[g][0]), __float_as_uint(v[g][1]),
+                                       __float_as_uint(v[g][2]), __float_as_uint(v[g][3])};
+            __builtin_amdgcn_raw_buffer_store_b128(w4, pres, off[g], (uint32_t)out_plane * sstride,
+                                                   kCachePolicySC1);
+            continue;
           }
 #pragma unroll
-        for (int g = 0; g < kG; ++g)
+          for (int q = 0; q < 4; ++q)
+            if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
+          // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread; plain
+          // outputs leave as one 16- or 8-byte store of the 4 columns.
+          if (ACT) {
+            store_act_quad(a.y, a.yt, m, n, a.N, v[g][0], v[g][1], v[g][2], v[g][3]);
+          } else if (a.yt == AWQ_F32) {
+            *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n) =
+                f32x4_t{v[g][0], v[g][1], v[g][2], v[g][3]};
+          } else if (a.yt == AWQ_F16) {
+            typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n) =
+                h4_t{(_Float16)v[g][0], (_Float16)v[g][1], (_Float16)v[g][2], (_Float16)v[g][3]};
+          } else {
 #pragma unroll
-          for (int b = 0; b < kSB; ++b) {
-            const bool live = sp + b < a.splits;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) v[g][q] += live ? t[g][b][q] : 0.f;
+            for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, 0, m, n + q, a.N, v[g][q], 0.f);
           }
-      }
-#pragma unroll
-      for (int g = 0; g < kG; ++g) {
-        if (!ok[g]) continue;
-        const int e4 = base + g * kTh + tid;
-        const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
-        // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread; plain
-        // outputs leave as one 16- or 8-byte store of the 4 columns.
-        if (ACT) {
-          store_act_quad(a.y, a.yt, m, n, a.N, v[g][0], v[g][1], v[g][2], v[g][3]);
-        } else if (a.yt == AWQ_F32) {
-          *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n) =
-              f32x4_t{v[g][0], v[g][1], v[g][2], v[g][3]};
-        } else if (a.yt == AWQ_F16) {
-          typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
-          *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n) =
-              h4_t{(_Float16)v[g][0], (_Float16)v[g][1], (_Float16)v[g][2], (_Float16)v[g][3]};
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, 0, m, n + q, a.N, v[g][q], 0.f);
         }
       }
+    };
+    if (tree) {
+      const int grp = split / a.gsize, gbeg = grp * a.gsize, gn = min(a.gsize, a.splits - gbeg);
+      if (!arrive(grp, gn)) return;
+      reduce(gbeg, gn, a.splits + grp);
+      if (!arrive(a.ngroups, a.ngroups)) return;
+      reduce(a.splits, a.ngroups, -1);
+    } else {
+      if (!arrive(0, a.splits)) return;
+      reduce(0, a.splits, -1);
     }
-    if (tid == 0)
-      __hip_atomic_store(&a.counters[chunk * kCtrStride], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   if constexpr (ACT) {
@@ -635,7 +669,8 @@ void launch_mt(const GemmProblem& p) {
     sps = (total_steps + splits - 1) / splits;
   }
   splits = (total_steps + sps - 1) / sps;
-  while (splits > 1 && (int64_t)splits * p.rows * p.N * 4 >= (1ll << 32)) {
+  // (planes, with the two-level sum's extra ones, below 4 GB: splits + 2 sqrt(splits) < 2 splits)
+  while (splits > 1 && (int64_t)2 * splits * p.rows * p.N * 4 >= (1ll << 32)) {
     --splits;
     sps = (total_steps + splits - 1) / splits;
     splits = (total_steps + sps - 1) / sps;
@@ -661,11 +696,32 @@ void launch_mt(const GemmProblem& p) {
   // XCD mapping only where grid.x keeps the XCD of a workgroup independent of
   // its split (chunks % 8 == 0) and each XCD's run covers whole 128-byte lines.
   a.xcd_chunks = (CW == 64 && chunks % 8 == 0 && (chunks / 8) % 4 == 0) ? chunks : 0;
+  a.gsize = splits;
+  a.ngroups = 1;
   if (splits > 1) {
+    // Two-level split sum (groups of g splits, g the smallest with g * g >=
+    // splits) on deep K: 12 or more splits. Measured (us, one level / two):
+    // 14336 -> 4096 at M = 17 / 24 / 64 (16 splits) 20.8 / 21.6 / 29.6 ->
+    // 20.2 / 20.7 / 27.5; 28672 -> 4096 at M = 64 41.5 -> 40.6. (More
+    // splits stay slower with it: 20..32 splits at 14336 -> 4096, M = 64,
+    // 37..43 us.) AWQ_SKINNY_TREE=0 / 1 forces one level / two (3 or more
+    // splits).
+    const int force = tuning(kTuneSkinnyTree, -1);
+    if (force != 0 && splits >= 3 && (force == 1 || splits >= 12)) {
+      int g = 1;
+      while (g * g < splits) ++g;
+      const int ng = (splits + g - 1) / g;
+      if (ng > 1) {
+        a.gsize = g;
+        a.ngroups = ng;
+      }
+    }
+    const int planes = splits + (a.ngroups > 1 ? a.ngroups : 0);
+    const int cpc = a.ngroups > 1 ? a.ngroups + 1 : 1;
     a.counters = static_cast<uint32_t*>(
-        ws_get(p, (size_t)chunks * kCtrStride * sizeof(uint32_t), kWsCounters));
+        ws_get(p, (size_t)chunks * cpc * kCtrStride * sizeof(uint32_t), kWsCounters));
     a.partial = static_cast<float*>(
-        ws_get(p, (size_t)splits * p.rows * p.N * sizeof(float), kWsPartials));
+        ws_get(p, (size_t)planes * p.rows * p.N * sizeof(float), kWsPartials));
   }
   ensure_dyn_smem((const void*)skinny_kernel<MT, false, BF, CW, WV>, (int)smem, "hipFuncSetAttribute(skinny)");
   ensure_dyn_smem((const void*)skinny_kernel<MT, true, BF, CW, WV>, (int)smem, "hipFuncSetAttribute(skinny)");

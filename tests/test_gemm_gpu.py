@@ -631,6 +631,25 @@ def test_skinny_every_split(dev, monkeypatch, cols, splits, x_dt, s_dt, g):
 
 
 @pytest.mark.parametrize("cols", list(SKINNY_COLS))
+@pytest.mark.parametrize("splits", [3, 7, 16, 64])
+@pytest.mark.parametrize("M,x_dt", [(17, "f16"), (100, "bf16"), (9, "f16")])
+def test_skinny_split_sum_two_levels(dev, monkeypatch, cols, splits, M, x_dt):
+    """The skinny kernel's two-level split-K sum (groups of splits, then the
+    groups), forced: against the oracle with bias and a ragged last chunk;
+    two calls give the same bits."""
+    _skinny_cols(monkeypatch, cols)
+    monkeypatch.setenv("AWQ_SKINNY", "1")
+    monkeypatch.setenv("AWQ_SKINNY_SPLITS", str(splits))
+    monkeypatch.setenv("AWQ_SKINNY_TREE", "1")
+    K, N, g = 4096, 2080, 64
+    x, qw, qz, sc, b = make_problem(M, K, N, g, x_dt=x_dt, s_dt=x_dt, bias=True)
+    y1 = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, x_dt, "f32")
+    y2 = _gemm_ptr(dev, x, qw, qz, sc, b, M, K, N, g, x_dt, x_dt, "f32")
+    assert torch.equal(y1, y2)
+    assert oracle.rel_l2(to_host(y1), _ref64(x, qw, qz, sc, b, g, x_dt, x_dt)) <= TOL_MFMA
+
+
+@pytest.mark.parametrize("cols", list(SKINNY_COLS))
 @pytest.mark.parametrize("M", [12, 48, 128])
 @pytest.mark.parametrize("splits", ["1", "3"])
 @pytest.mark.parametrize("x_dt,s_dt", [("f16", "f16"), ("bf16", "bf16"), ("bf16", "f16"), ("f16", "bf16")])

@@ -102,10 +102,11 @@ def test_silu_mul_every_route(dev, monkeypatch, M, x_dt, env):
     (3, "f16", 8192, {}),                        # 4x4x4 blocks, 16 waves, 16 K splits
     (4, "f32", 14336, {"AWQ_DECODE_TREE": "1"}),   # 4x4x4 blocks, two-level split sum
     (8, "f16", 14336, {"AWQ_DECODE_TREE": "1"}),   # 16-row tile, two-level split sum
+    (64, "f16", 14336, {"AWQ_SKINNY_TREE": "1", "AWQ_SKINNY_SPLITS": "16"}),  # skinny, two levels
 ])
 def test_silu_mul_decode_deep_k(dev, monkeypatch, M, x_dt, K, env):
     """SiLU epilogue after a split-K sum over more than 8 splits (shared by
-    thread groups), with a partial column chunk and bias."""
+    thread groups, or in two levels), with a partial column chunk and bias."""
     for k, v in env.items():
         monkeypatch.setenv(k, v)
     N, g = 2112, 128  # a multiple of 64 (the gate/up rule), not of 512
@@ -115,7 +116,8 @@ def test_silu_mul_decode_deep_k(dev, monkeypatch, M, x_dt, K, env):
     y = _launch(L.awq_gemm_silu_mul, dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, N // 2)
     assert np.isfinite(y).all()
     h = oracle.gemm_f64(host_f32(x, x_dt), qw, qz, host_f32(sc, s_dt), g, bias=b)
-    assert oracle.rel_l2(y, silu_mul64(h)) <= 2e-5
+    tol = 2e-5 if (x_dt == "f32" or M <= 8) else 4e-3  # the skinny route builds f16 weights
+    assert oracle.rel_l2(y, silu_mul64(h)) <= tol
     full = _launch(L.awq_gemm, dev, x, qw, qz, sc, b, M, K, N, g, x_dt, s_dt, N)
     assert oracle.rel_l2(y, silu_mul64(full)) <= 2e-6
 
