@@ -19,12 +19,13 @@ G = 128
 # (M, K, N, x dtype, smaller M for the second call): decode VALU with K
 # splits, 4x4x4 matrix-core decode, 16x16x32 decode tile, 9..16 rows, the
 # skinny kernel with K splits, large tiles with K splits, fp32 16-row slices,
-# a large-tile prefill with no split, and both matrix-core decode kernels
-# with the two-level split sum (28 splits over 8 column chunks).
+# a large-tile prefill with no split, both matrix-core decode kernels with
+# the two-level split sum (28 splits over 8 column chunks), and the skinny
+# kernel with it (16 splits).
 CASES = [(1, 4096, 4096, "f32", 1), (4, 4096, 14336, "f32", 2), (8, 8192, 8192, "f32", 5),
          (16, 4096, 4096, "f16", 9), (64, 4096, 14336, "f16", 24), (300, 1024, 1024, "f16", 130),
          (40, 4096, 4096, "f32", 17), (512, 4096, 4096, "f16", 256), (8, 14336, 4096, "f32", 6),
-         (4, 14336, 4096, "f32", 3)]
+         (4, 14336, 4096, "f32", 3), (64, 14336, 4096, "f16", 24)]
 
 
 def _i32(a, dev):
