@@ -408,9 +408,13 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
     if (!s_last) return;
-    if (threadIdx.x == 0)
-      __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+    // The counter is re-armed after the sum: issued earlier, the agent-scope
+    // store would sit ahead of the sum's loads in wave 0's in-order vmcnt.
+    auto rearm = [&]() {
+      if (threadIdx.x == 0)
+        __hip_atomic_store(&a.counters[chunk * kCounterStride], 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    };
     // More than 8 splits (deep K): 4-column pieces, the splits shared by
     // thread groups (grouped_split_sum), one round of loads instead of one
     // per 8 splits (14336 -> 4096 at one row: 28 splits).
@@ -420,6 +424,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
         // The slots are free: every thread read its slots before the arrival barrier.
         const f32x4_t r = grouped_split_sum<MT, kQ, 64 * WAVES / kQ>(
             a, reinterpret_cast<f32x4_t*>(&red[0][0][0]), rows, col_base, a.splits, 0, a.splits);
+        rearm();
         const int q = threadIdx.x;
         const int m = q / (kChunkCols / 4), n0 = col_base + 4 * (q % (kChunkCols / 4));
         if (q < kQ && m < rows && n0 < a.N) {
@@ -451,6 +456,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_kernel(GemvArgs a) {
         res[i] = v;
       }
     }
+    rearm();
   }
 
   // Adjacent threads hold adjacent columns, so a gate/up pair is this lane
@@ -604,7 +610,7 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, float (*red)[MV]
       }
     };
     // Publish the stored plane and count the arrival on counter ci of this
-    // chunk; true in the last of `expect` arrivals (which re-arms it).
+    // chunk; true in the last of `expect` arrivals.
     auto arrive = [&](int ci, int expect) -> bool {
       // Partials complete before the arrival (split-K handshake, awq_common.h).
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -615,9 +621,15 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, float (*red)[MV]
         s_last = (prev == (uint32_t)(expect - 1)) ? 1 : 0;
       }
       __syncthreads();
-      if (!s_last) return false;
-      if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return true;
+      return s_last != 0;
+    };
+    // Re-arm counter ci for the next call, after the sum (issued earlier, the
+    // agent-scope store would sit ahead of the sum's loads in wave 0's
+    // in-order vmcnt).
+    auto rearm = [&](int ci) {
+      if (tid == 0)
+        __hip_atomic_store(&a.counters[(chunk * cpc + ci) * kCounterStride], 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     };
     // res = the sum of planes p0 .. p0 + np - 1, in order.
     auto sum_planes = [&](int p0, int np) {
@@ -673,12 +685,15 @@ __device__ __forceinline__ void finish_chunk(const GemvArgs& a, float (*red)[MV]
       const int grp = split / a.gsize, gbeg = grp * a.gsize, gn = min(a.gsize, a.splits - gbeg);
       if (!arrive(grp, gn)) return;
       sum_planes(gbeg, gn);
+      rearm(grp);
       store_plane(a.splits + grp);
       if (!arrive(a.ngroups, a.ngroups)) return;
       sum_planes(a.splits, a.ngroups);
+      rearm(a.ngroups);
     } else {
       if (!arrive(0, a.splits)) return;
       sum_planes(0, a.splits);
+      rearm(0);
     }
   }
 

@@ -489,8 +489,9 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
     // publishes that sum as plane splits + group through the same handshake
     // (one more arrival counter per group), and the last group sums the
     // group planes in order. Both trees are fixed, so results stay
-    // deterministic.
-    const bool tree = a.ngroups > 1;
+    // deterministic. 256-column chunks only (the deep-K shapes that reach
+    // 12 splits; 64-column chunks stay at 8 or fewer).
+    const bool tree = CW == 256 && a.ngroups > 1;
     const int cpc = tree ? a.ngroups + 1 : 1;  // counters per chunk
     auto arrive = [&](int ci, int expect) -> bool {
       // Partials complete before the arrival (split-K handshake, awq_common.h).
@@ -502,9 +503,16 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
         *s_last = (prev == (uint32_t)(expect - 1)) ? 1 : 0;
       }
       __syncthreads();
-      if (!*s_last) return false;
-      if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return true;
+      return *s_last != 0;
+    };
+    // Re-arm counter ci for the next call, after the sum: issued earlier, the
+    // agent-scope store sits ahead of the sum's loads in wave 0's in-order
+    // vmcnt and delays its first wait (64-column chunks at M = 64..128:
+    // 20-39 % slower).
+    auto rearm = [&](int ci) {
+      if (tid == 0)
+        __hip_atomic_store(&a.counters[(chunk * cpc + ci) * kCtrStride], 0u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     };
     // Sum planes p0 .. p0 + np - 1 of this chunk in order: 4 consecutive
     // columns per 16-byte load (N % 32 == 0 keeps them inside a row), kG
@@ -592,11 +600,85 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
       const int grp = split / a.gsize, gbeg = grp * a.gsize, gn = min(a.gsize, a.splits - gbeg);
       if (!arrive(grp, gn)) return;
       reduce(gbeg, gn, a.splits + grp);
+      rearm(grp);
       if (!arrive(a.ngroups, a.ngroups)) return;
       reduce(a.splits, a.ngroups, -1);
+      rearm(a.ngroups);
     } else {
+      // One level: the loop kept in this form (the shared sum above, used
+      // here too, changed the 64-column kernels' register allocation and put
+      // a vmcnt(0) wait before each partial store: 20-39 % slower at 64..128
+      // rows).
       if (!arrive(0, a.splits)) return;
-      reduce(0, a.splits, -1);
+      // Sum the splits of this chunk in split order: 4 consecutive columns per
+      // 16-byte load (N % 32 == 0 keeps them inside a row), kG column groups
+      // per thread per round, kSB splits deep -- kG kSB loads in flight, so
+      // most chunks take one round. Slots past the chunk, M or the splits are
+      // loaded clamped and not used.
+      for (int base = 0; base < total4; base += kTh * kG) {
+        uint32_t off[kG];
+        bool ok[kG];
+        float v[kG][4];
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          const int e4 = base + g * kTh + tid;
+          const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
+          ok[g] = e4 < total4 && n < a.N;
+          off[g] = (uint32_t)(((int64_t)min(m, a.M - 1) * a.N + min(n, a.N - 4)) * 4);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) v[g][q] = 0.f;
+        }
+        for (int sp = 0; sp < a.splits; sp += kSB) {
+          float t[kG][kSB][4];
+#pragma unroll
+          for (int g = 0; g < kG; ++g)
+#pragma unroll
+            for (int b = 0; b < kSB; ++b) {
+              const u32x4_t w4 = __builtin_amdgcn_raw_buffer_load_b128(
+                  pres, off[g], (uint32_t)min(sp + b, a.splits - 1) * sstride, kCachePolicySC1);
+              // through plain scalars: __builtin_bit_cast of a vector element
+              // directly reads the wrong element (hipcc 7.2)
+              const uint32_t e0 = w4[0], e1 = w4[1], e2 = w4[2], e3 = w4[3];
+              t[g][b][0] = __uint_as_float(e0);
+              t[g][b][1] = __uint_as_float(e1);
+              t[g][b][2] = __uint_as_float(e2);
+              t[g][b][3] = __uint_as_float(e3);
+            }
+#pragma unroll
+          for (int g = 0; g < kG; ++g)
+#pragma unroll
+            for (int b = 0; b < kSB; ++b) {
+              const bool live = sp + b < a.splits;
+#pragma unroll
+              for (int q = 0; q < 4; ++q) v[g][q] += live ? t[g][b][q] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          if (!ok[g]) continue;
+          const int e4 = base + g * kTh + tid;
+          const int m = e4 / kQuads, n = chunk * CW + 4 * (e4 % kQuads);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (a.bias) v[g][q] += load_f32_any(a.bias, n + q, a.bt);
+          // n % 4 == 0: the gate/up pairs are (q, q ^ 1) of this thread; plain
+          // outputs leave as one 16- or 8-byte store of the 4 columns.
+          if (ACT) {
+            store_act_quad(a.y, a.yt, m, n, a.N, v[g][0], v[g][1], v[g][2], v[g][3]);
+          } else if (a.yt == AWQ_F32) {
+            *reinterpret_cast<f32x4_t*>(static_cast<float*>(a.y) + (int64_t)m * a.N + n) =
+                f32x4_t{v[g][0], v[g][1], v[g][2], v[g][3]};
+          } else if (a.yt == AWQ_F16) {
+            typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<h4_t*>(static_cast<f16_t*>(a.y) + (int64_t)m * a.N + n) =
+                h4_t{(_Float16)v[g][0], (_Float16)v[g][1], (_Float16)v[g][2], (_Float16)v[g][3]};
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) store_out(a.y, a.yt, 0, m, n + q, a.N, v[g][q], 0.f);
+          }
+        }
+      }
+      rearm(0);
     }
     return;
   }
@@ -700,14 +782,15 @@ void launch_mt(const GemmProblem& p) {
   a.ngroups = 1;
   if (splits > 1) {
     // Two-level split sum (groups of g splits, g the smallest with g * g >=
-    // splits) on deep K: 12 or more splits. Measured (us, one level / two):
+    // splits) on deep K: 12 or more splits, 256-column chunks. Measured (us,
+    // one level / two):
     // 14336 -> 4096 at M = 17 / 24 / 64 (16 splits) 20.8 / 21.6 / 29.6 ->
     // 20.2 / 20.7 / 27.5; 28672 -> 4096 at M = 64 41.5 -> 40.6. (More
     // splits stay slower with it: 20..32 splits at 14336 -> 4096, M = 64,
     // 37..43 us.) AWQ_SKINNY_TREE=0 / 1 forces one level / two (3 or more
     // splits).
     const int force = tuning(kTuneSkinnyTree, -1);
-    if (force != 0 && splits >= 3 && (force == 1 || splits >= 12)) {
+    if (CW == 256 && force != 0 && splits >= 3 && (force == 1 || splits >= 12)) {
       int g = 1;
       while (g * g < splits) ++g;
       const int ng = (splits + g - 1) / g;
