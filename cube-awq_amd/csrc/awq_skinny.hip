@@ -505,10 +505,9 @@ __global__ __launch_bounds__(64 * WV) void skinny_kernel(SkinnyArgs a) {
       __syncthreads();
       return *s_last != 0;
     };
-    // Re-arm counter ci for the next call, after the sum: issued earlier, the
-    // agent-scope store sits ahead of the sum's loads in wave 0's in-order
-    // vmcnt and delays its first wait (64-column chunks at M = 64..128:
-    // 20-39 % slower).
+    // Re-arm counter ci for the next call, after the sum (issued earlier, the
+    // agent-scope store would sit ahead of the sum's loads in wave 0's
+    // in-order vmcnt).
     auto rearm = [&](int ci) {
       if (tid == 0)
         __hip_atomic_store(&a.counters[(chunk * cpc + ci) * kCtrStride], 0u, __ATOMIC_RELAXED,
