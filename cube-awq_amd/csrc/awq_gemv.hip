@@ -35,8 +35,10 @@
 //    (grid.y = splits), each writes its partial and the last to arrive sums
 //    them in a fixed order (split order; with more than 8 splits, contiguous
 //    split ranges per thread group, then the groups in order:
-//    grouped_split_sum); arrival counters sit on separate 256-byte lines so
-//    chunks do not serialise on one line.
+//    grouped_split_sum; on the matrix-core kernels with deep K over few
+//    chunks, two levels: groups of about sqrt(splits) splits summed by their
+//    last workgroup, then the groups, finish_chunk); arrival counters sit on
+//    separate 256-byte lines so chunks do not serialise on one line.
 //
 // Algorithmic HBM bytes per call: K*N/2 (qweight) + (K/g)*(N/8)*4 (qzeros) +
 // (K/g)*N*sizeof(scale) + M*K*sizeof(x) + M*N*sizeof(y).
