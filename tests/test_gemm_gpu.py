@@ -494,6 +494,20 @@ def test_decode_m4_every_configuration(dev, monkeypatch, waves, rpw, x_dt, s_dt,
     assert oracle.rel_l2(to_host(y), ref) <= TOL_FP32
 
 
+@pytest.mark.parametrize("K,N,g", [(64, 32, 64), (192, 64, 64), (4160, 544, 64), (320, 4096, 64),
+                                   (30720, 544, 128), (128, 28672, 128)])
+@pytest.mark.parametrize("x_dt", ["f32", "f16", "bf16"])
+def test_decode_one_row_edge_shapes(dev, K, N, g, x_dt):
+    """One row through the launch-shape rule at its edges: one 32-column
+    chunk (most lanes clamped), waves whose rows start past K, the shortest
+    runs (16 waves x 8 rows), deep K over few chunks (16 waves x 16 rows,
+    120 splits: the grouped sum) and one split over many chunks."""
+    x, qw, qz, sc, b = make_problem(1, K, N, g, x_dt=x_dt, s_dt="f16", bias=True)
+    y = to_host(_gemm_ptr(dev, x, qw, qz, sc, b, 1, K, N, g, x_dt, "f16", "f32"))
+    assert np.isfinite(y).all()
+    assert oracle.rel_l2(y, _ref64(x, qw, qz, sc, b, g, x_dt, "f16")) <= TOL_FP32
+
+
 @pytest.mark.parametrize("K,N,g", [(64, 32, 64), (192, 64, 64), (4160, 544, 64), (320, 4096, 64)])
 @pytest.mark.parametrize("x_dt", ["f32", "f16"])
 @pytest.mark.parametrize("M", [2, 3, 4])
